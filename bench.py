@@ -1,0 +1,231 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X MoE block (BASELINE.json metric).
+
+Headline (`value`): decode tokens/s at B=1 through the 40-layer MoE-only stack
+each step is one token through 40 layers of
+x_{l+1} = x_l + MoE_l(RMSNorm(x_l)), all 40 x 256 experts resident in one
+HBM arena, inputs resident in HBM before timing.  Also reported:
+  * hbm_gbs: algorithmic bytes/token (40 x 19,619,840 B) x tokens/s;
+  * prefill512_tflops: BASELINE config 3 (512 tokens, one layer, Zipf s=1
+    router bias), 29.53 GFLOP per call / time;
+  * roofline: the dominant decode kernel (routed gate/up, k_gu) timed with HIP
+    events on its own stream over a profiled pass of the same workload;
+  * cpu_baseline: the CPU AVX2 restatement of the reference CPU MoE path
+    (oracle/qe_oracle.cpp) on a bounded sample, host cores, same process.
+Weights are random-init from the seeded generator (no checkpoints offline).
+"""
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(REPO, "qe-qwen36-b50_amd"))
+
+import numpy as np  # noqa: E402
+
+METRIC = "MoE decode tokens/s + HBM GB/s at B=1; prefill-512 MoE TFLOPS (1 GPU)"
+EXPERT_BYTES = 1769472
+GU_BYTES = 2 * 512 * 1152              # gate + up rows of one expert
+LAYER_BYTES_B1 = 8 * EXPERT_BYTES + 1024 * 2176 + 2048 * 544 + 257 * 2048 * 4 + 2 * 8192  # 19,619,840
+N_LAYERS = 40
+FLOP_PER_TOKEN = 8 * 6291456 + 6291456 + 2 * 257 * 2048  # 57,675,776
+HBM_PEAK = 8.0e12
+SEED = 0x51E3_6B50
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def timed(torch, fn, steps, stream):
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for _ in range(steps):
+        fn()
+    b.record(stream)
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / steps
+
+
+def cpu_baseline(n_layers_sample, tokens_sample, threads):
+    """Reference CPU MoE path (AVX2 port) on a bounded sample: tokens_sample
+    tokens, each through n_layers_sample distinct layers (B=1 decode), all on
+    host cores.  Returns tokens/s scaled to the 40-layer stack."""
+    sys.path.insert(0, os.path.join(REPO, "oracle"))
+    import oracle as O
+
+    layers = [O.SynthLayer(SEED + 7, l) for l in range(n_layers_sample)]
+    pn = np.ones(2048, np.float32)
+    xs = [O.gen_x(SEED + 7, 1000 + t, 1) for t in range(tokens_sample)]
+    # pre-generate the experts every (token, layer) will route to, outside the timing
+    plans = []
+    for t in range(tokens_sample):
+        h = xs[t]
+        for L in layers:
+            r = O.moe_layer(L, h, norm=True, residual=True)
+            plans.append(r["ids"])
+            h = r["out"]
+    ptr_sets = []
+    for L in layers:
+        ptrs = (ctypes.c_void_p * 256)()
+        ptr_sets.append(ptrs)
+    for i, ids in enumerate(plans):
+        L = layers[i % n_layers_sample]
+        for e, blob in L.experts(ids).items():
+            ptr_sets[i % n_layers_sample][e] = blob.ctypes.data
+    total = 0.0
+    for t in range(tokens_sample):
+        h = xs[t]
+        for li, L in enumerate(layers):
+            sec, h = O.baseline_layer(h, pn, L, ptr_sets[li], 1, threads)
+            total += sec
+    per_layer = total / (tokens_sample * n_layers_sample)
+    return 1.0 / (per_layer * N_LAYERS), total
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying a HIP graph")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--cpu-layers", type=int, default=8)
+    ap.add_argument("--cpu-tokens", type=int, default=8)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
+              "multi-GPU expert sharding is design-only, see DESIGN.md", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import qe_moe
+
+    assert torch.cuda.is_available(), "no GPU visible"
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream()
+
+    # ---------------- config 2: 40-layer decode, B=1 ----------------
+    log("building 40-layer arena (18.12 GB) from the seeded generator")
+    m = qe_moe.MoE(n_layers=N_LAYERS, t_max=8)
+    for l in range(N_LAYERS):
+        m.synth_layer(l, SEED, None, stream=stream)
+    x = torch.empty(1, 2048, device=dev)
+    qe_moe.synth_x(SEED, 0, x, x.numel(), stream=stream)
+    y = torch.empty_like(x)
+    torch.cuda.synchronize()
+
+    def step_eager():
+        m.forward_stack(0, N_LAYERS, x, y, 1, stream=torch.cuda.current_stream())
+
+    step_eager()
+    torch.cuda.synchronize()
+    y_eager = y.clone()
+    step = step_eager
+    graph_used = False
+    if not args.no_graph:
+        g = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            step_eager()
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g):
+            step_eager()
+        ok = True
+        for _ in range(3):  # every replay must equal the eager result
+            y.zero_()
+            g.replay()
+            torch.cuda.synchronize()
+            ok = ok and torch.equal(y, y_eager)
+            step_eager()
+            torch.cuda.synchronize()
+        if ok:
+            step, graph_used = g.replay, True
+        else:
+            log("graph replay differs from eager: timing eager launches")
+    log(f"decode: warmup {args.warmup}, timed {args.steps} (graph={graph_used})")
+    for _ in range(args.warmup):
+        step()
+    ms = timed(torch, step, args.steps, torch.cuda.current_stream())
+    tok_s = 1000.0 / ms
+    assert torch.equal(y, y_eager), "timed output differs from the eager reference"
+
+    # per-kernel HIP events over a profiled pass of the same workload (eager launches)
+    m.profile(True)
+    prof_steps = min(args.steps, 100)
+    for _ in range(prof_steps):
+        step_eager()
+    torch.cuda.synchronize()
+    prof = m.profile_read()
+    m.profile(False)
+    gu_ms, gu_n = prof["k_gu"]
+    gu_avg_s = gu_ms / gu_n / 1e3
+    gu_bytes = 8 * GU_BYTES + 2048 + 256 + 8 * 512 * 4  # weights + xq/xs in + h out
+    achieved = gu_bytes / gu_avg_s
+    kernels = {k: {"avg_us": round(v[0] / v[1] * 1e3, 3), "launches": v[1]} for k, v in prof.items()}
+    del m
+    torch.cuda.empty_cache()
+
+    # ---------------- config 3: prefill 512, one layer ----------------
+    pre = {}
+    if not args.no_prefill:
+        sys.path.insert(0, os.path.join(REPO, "oracle"))
+        bias = np.empty(256, np.float32)
+        import oracle as O
+
+        bias = O.gen_zipf_bias(SEED, 0, 1.0)
+        mp = qe_moe.MoE(n_layers=1, t_max=512)
+        mp.synth_layer(0, SEED, bias, stream=stream)
+        xp = torch.empty(512, 2048, device=dev)
+        qe_moe.synth_x(SEED, 3, xp, xp.numel(), stream=stream)
+        yp = torch.empty_like(xp)
+        for _ in range(3):
+            mp.forward_normed(0, xp, yp, 512, stream=torch.cuda.current_stream())
+        pms = timed(torch, lambda: mp.forward_normed(0, xp, yp, 512, stream=torch.cuda.current_stream()),
+                    max(5, args.steps // 10), torch.cuda.current_stream())
+        r = mp.routing(512)
+        cnt = np.diff(r["off"])
+        pre = {"prefill512_ms": round(pms, 4), "prefill512_tflops": round(512 * FLOP_PER_TOKEN / (pms / 1e3) / 1e12, 3),
+               "prefill512_routing": {"distinct_experts": int(np.count_nonzero(cnt)), "max_tokens_per_expert": int(cnt.max()),
+                                      "top8_share": round(float(np.sort(cnt)[-8:].sum() / cnt.sum()), 4),
+                                      "experts_lt4_tokens": int(((cnt > 0) & (cnt < 4)).sum())}}
+        del mp
+
+    # ---------------- CPU baseline ----------------
+    cpu = None
+    if not args.no_cpu_baseline:
+        threads = min(os.cpu_count() or 1, 16)
+        log(f"cpu baseline: {args.cpu_tokens} tokens x {args.cpu_layers} layers, {threads} threads")
+        cpu_tok_s, cpu_sec = cpu_baseline(args.cpu_layers, args.cpu_tokens, threads)
+        cpu = {"value": round(cpu_tok_s, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
+               "sample": f"{args.cpu_tokens} tokens x {args.cpu_layers} distinct layers of the config-2 stack (B=1 decode, "
+                         f"full layer: norm, router, top-8, dispatch, int8 experts, Q8 shared, combine, residual), "
+                         f"{cpu_sec:.2f} s of CPU time, scaled to 40 layers"}
+
+    out = {
+        "metric": METRIC, "value": round(tok_s, 2), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "int8", "data": "synthetic (seeded random-init weights of the config shapes)",
+        "config": {"workload": "cfg2: 40-layer MoE-only stack, decode B=1, 1 token per step", "layers": N_LAYERS,
+                   "tokens_per_step": 1, "experts": 256, "top_k": 8, "hip_graph": graph_used},
+        "hbm_gbs": round(N_LAYERS * LAYER_BYTES_B1 * tok_s / 1e9, 2),
+        "hbm_frac": round(N_LAYERS * LAYER_BYTES_B1 * tok_s / HBM_PEAK, 4),
+        **pre,
+        "roofline": {"kernel": "k_gu (routed gate/up + SwiGLU, B=1)", "bound": "hbm", "achieved": round(achieved / 1e9, 2),
+                     "peak": HBM_PEAK / 1e9, "unit": "GB/s", "frac": round(achieved / HBM_PEAK, 4), "traffic": None,
+                     "bytes_per_launch": gu_bytes, "avg_us": round(gu_avg_s * 1e6, 3)},
+        "kernels": kernels,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

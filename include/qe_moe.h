@@ -1,0 +1,136 @@
+/* qe_moe.h -- C ABI of the MI355X (gfx950) Qwen3.6-35B-A3B MoE block.
+ *
+ * One context owns, on one GPU, a flat expert arena holding every routed
+ * expert of every layer (n_layers x 256 blobs in the reference pack layout),
+ * the per-layer dense weights (post-norm, router + shared-gate rows, Q8 shared
+ * expert) and all scratch for up to t_max tokens per call.  It replaces the
+ * MoE sections of the reference engine:
+ *   Engine::moe_batched ........... engine/qe.cpp:1957-2047 (prefill / chunks)
+ *   MoE block of Engine::decode ... engine/qe.cpp:2466-2572 (B = 1)
+ *   MoE block of decode_multi<NT> . engine/qe.cpp:1653-1737 (NT <= 8)
+ * and the VRAM/RAM expert residency tables (engine/qe.cpp:927-931,
+ * 1131-1198), which become the flat arena: expert e of layer l lives at
+ * arena + (l*256 + e) * qe_moe_expert_bytes().
+ *
+ * Conventions: plain pointers and sizes; activations are device pointers to
+ * fp32 [T][2048] row-major; `stream` is a hipStream_t (NULL = default
+ * stream).  Calls enqueue work on `stream` and return without a host sync,
+ * except qe_moe_get_routing, which copies to the host.  A context is used by
+ * one host thread at a time, and calls on one context must not overlap on
+ * different streams (the reference's single-engine-thread rule,
+ * engine/qe.cpp:877, 3162).  Every entry point returns 0 or a negative
+ * QE_ERR_* code; qe_moe_last_error() describes the last failure of the
+ * calling thread.  The reference has no error returns (it exits,
+ * engine/qe.cpp:1022); these codes replace that.
+ */
+#ifndef QE_MOE_H
+#define QE_MOE_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QE_OK 0
+#define QE_ERR_ARG (-1)   /* bad argument (null pointer, layer or T out of range) */
+#define QE_ERR_HIP (-2)   /* a HIP runtime call failed */
+#define QE_ERR_OOM (-3)   /* device allocation failed */
+#define QE_ERR_STATE (-4) /* context not ready (weights of the layer never set) */
+
+typedef struct qe_moe_ctx qe_moe_ctx;
+
+/* Create a context on `device` for n_layers layers and calls of up to t_max
+ * tokens.  Allocates the arena (n_layers * 452,984,832 B) and scratch.
+ * Replaces Engine::Engine's upload/arena/scratch set-up (engine/qe.cpp:1038-1244). */
+int qe_moe_create(int device, int n_layers, int t_max, qe_moe_ctx **out);
+int qe_moe_destroy(qe_moe_ctx *ctx);
+
+/* Bytes of one routed expert blob: gate[512] | up[512] | down[2048] NL4 rows
+ * (engine/pack.h:40-42, exp_bytes()). */
+size_t qe_moe_expert_bytes(void);
+
+/* Copy n_experts blobs (expert ids first..first+n-1 of `layer`) into the arena,
+ * from host (src_on_device = 0) or device memory.  A pack's blk.N.experts
+ * entry (engine/qconv.cpp:202-228) copies in as is.  Replaces the arena/host
+ * expert copies of engine/qe.cpp:1172-1194. */
+int qe_moe_upload_experts(qe_moe_ctx *ctx, int layer, int first, int n_experts, const void *src, int src_on_device,
+                          void *stream);
+
+/* Set a layer's dense weights (engine/qe.cpp:855-870 Layer fields, uploaded at
+ * :1053-1057): post_norm fp32[2048]; router fp32[257][2048] (rows 0..255 the
+ * expert router, row 256 the shared-expert gate, as upload({router, sh_gate})
+ * builds it at :1055); bias fp32[256] added to logits 0..255 (NULL = none);
+ * sh_gu Q8 [1024 rows x 2048] (gate rows 0..511, up rows 512..1023);
+ * sh_down Q8 [2048 rows x 512].  Any pointer may be NULL to keep the current
+ * contents.  Sources are host or device memory per src_on_device. */
+int qe_moe_set_dense(qe_moe_ctx *ctx, int layer, const float *post_norm, const float *router, const float *bias,
+                     const void *sh_gu, const void *sh_down, int src_on_device, void *stream);
+
+/* Full MoE section: x = x2 + MoE(RMSNorm(x2) * post_norm), T tokens.
+ * Replaces Engine::moe_batched (engine/qe.cpp:1957) and the MoE blocks of
+ * decode (:2466-2572) / decode_multi (:1653-1737).  x may not alias x2. */
+int qe_moe_forward(qe_moe_ctx *ctx, int layer, const float *x2, float *x, int T, void *stream);
+
+/* MoE on already-normalised input, no residual: y = MoE(xn).  The "one MoE
+ * layer" of the benchmark configurations; the same kernels as qe_moe_forward
+ * with the norm and the residual switched off. */
+int qe_moe_forward_normed(qe_moe_ctx *ctx, int layer, const float *xn, float *y, int T, void *stream);
+
+/* Layers first..first+n_layers-1 in sequence, each x_{l+1} = x_l +
+ * MoE_l(RMSNorm(x_l)): the per-layer MoE steps of the decode loop
+ * (engine/qe.cpp:2241-2572) with attention/DeltaNet left out.  x_in is not
+ * modified; the result lands in x_out; the context's ping-pong buffer holds
+ * intermediate layers. */
+int qe_moe_forward_stack(qe_moe_ctx *ctx, int first_layer, int n_layers, const float *x_in, float *x_out, int T,
+                         void *stream);
+
+/* Routing of the last forward call (synchronises `stream`, copies to host):
+ * ids int32[T][8] (k = 0 largest), weights fp32[T][8], shared gate fp32[T],
+ * off int32[257] (exclusive per-expert prefix), pairs int32[T*8] (pair
+ * p = t*8+k grouped by expert, ascending p inside an expert), shared-expert
+ * output fp32[T][2048] before gating.  Any output may be NULL.  The parity
+ * sink of the reference's IDB/WB/SHG/PAIRS/OFF/SD buffers (engine/qe.cpp:1966-1978). */
+int qe_moe_get_routing(qe_moe_ctx *ctx, int T, int32_t *ids, float *wts, float *shg, int32_t *off, int32_t *pairs,
+                       float *shared_out, void *stream);
+
+/* Token-to-expert dispatch alone on caller-supplied ids (device int32[T][8],
+ * each in 0..255): per-expert histogram, exclusive scan and the stable
+ * permutation of Engine::moe_batched (engine/qe.cpp:1965-1976), run on the
+ * GPU; read the result with qe_moe_get_routing (off, pairs). */
+int qe_moe_dispatch(qe_moe_ctx *ctx, const int32_t *ids, int T, void *stream);
+
+/* Router logits fp32[T][257] of the last forward call (synchronises `stream`,
+ * copies to host): the parity sink of the reference's RL buffer
+ * (engine/qe.cpp:1959). */
+int qe_moe_get_logits(qe_moe_ctx *ctx, int T, float *logits, void *stream);
+
+/* Per-kernel timing, the counterpart of the reference's QE_PROF phase timers
+ * (engine/qe.cpp:1246-1251; MoE phases at :1964-2046, :1662-1737): when
+ * enabled, every kernel launch of the forward calls is bracketed by two HIP
+ * events on its own stream.  qe_moe_profile_read sums the elapsed time and
+ * launch count per kernel id (arrays of at least QE_MOE_NPROF entries), then
+ * clears the record; qe_moe_profile_name names an id. */
+#define QE_MOE_NPROF 12
+int qe_moe_profile(qe_moe_ctx *ctx, int enable);
+int qe_moe_profile_read(qe_moe_ctx *ctx, double *ms, int *launches, int n);
+const char *qe_moe_profile_name(int id);
+
+/* Device pointer of a layer's expert arena (256 blobs), for callers that fill
+ * it in place. */
+int qe_moe_arena_ptr(qe_moe_ctx *ctx, int layer, void **dev);
+
+/* Fill a layer (experts + dense weights) on the device from the seeded
+ * synthetic generator; bias (host fp32[256], NULL = none) is stored as the
+ * router bias.  Benchmark/test set-up, no reference counterpart: the
+ * reference loads real weights from a pack. */
+int qe_moe_synth_layer(qe_moe_ctx *ctx, int layer, uint64_t seed, const float *bias, void *stream);
+/* Fill n fp32 activations N(0,1) of activation set `inst` on the device. */
+int qe_moe_synth_x(uint64_t seed, int inst, float *dev_out, int64_t n, void *stream);
+
+const char *qe_moe_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,325 @@
+// C ABI of the MoE block (include/qe_moe.h): context, flat expert arena,
+// per-layer dense weights, scratch, and the forward entry points.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <string>
+#include <vector>
+
+#include "../../include/qe_moe.h"
+#include "qe_kernels.h"
+
+static thread_local std::string g_err;
+
+static int fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+static int fail(int code, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+#define HIP_TRY(expr)                                                                             \
+    do {                                                                                          \
+        hipError_t e_ = (expr);                                                                   \
+        if (e_ != hipSuccess) return fail(QE_ERR_HIP, "%s: %s", #expr, hipGetErrorString(e_));    \
+    } while (0)
+
+struct qe_moe_ctx {
+    int device = 0, n_layers = 0, t_max = 0;
+    uint8_t *arena = nullptr;    // n_layers * 256 * EXPERT_BYTES
+    float *router = nullptr;     // n_layers * 257 * 2048
+    float *bias = nullptr;       // n_layers * 256
+    uint8_t *sh_gu = nullptr;    // n_layers * SH_GU_BYTES
+    uint8_t *sh_dn = nullptr;    // n_layers * SH_DN_BYTES
+    float *post_norm = nullptr;  // n_layers * 2048
+    std::vector<uint8_t> has_bias, ready;
+    QeScratch S{};
+    QeProf prof;
+    float *pingpong[2] = {nullptr, nullptr};
+    std::vector<void *> allocs;
+};
+
+static int dalloc(qe_moe_ctx *c, void **p, size_t bytes) {
+    if (hipMalloc(p, bytes) != hipSuccess) {
+        *p = nullptr;
+        return fail(QE_ERR_OOM, "hipMalloc(%zu) failed", bytes);
+    }
+    c->allocs.push_back(*p);
+    return QE_OK;
+}
+
+static void free_all(qe_moe_ctx *c) {
+    for (void *p : c->allocs) (void)hipFree(p);
+    c->allocs.clear();
+}
+
+static QeLayerPtrs layer_ptrs(const qe_moe_ctx *c, int l) {
+    QeLayerPtrs L;
+    L.arena = c->arena + (size_t)l * QE_LAYER_EXPERT_BYTES;
+    L.router = c->router + (size_t)l * QE_ROUTER_ROWS * QE_D;
+    L.bias = c->has_bias[l] ? c->bias + (size_t)l * QE_N_EXPERT : nullptr;
+    L.sh_gu = c->sh_gu + (size_t)l * QE_SH_GU_BYTES;
+    L.sh_dn = c->sh_dn + (size_t)l * QE_SH_DN_BYTES;
+    L.post_norm = c->post_norm + (size_t)l * QE_D;
+    return L;
+}
+
+extern "C" {
+
+const char *qe_moe_last_error(void) { return g_err.c_str(); }
+
+size_t qe_moe_expert_bytes(void) { return QE_EXPERT_BYTES; }
+
+int qe_moe_create(int device, int n_layers, int t_max, qe_moe_ctx **out) {
+    if (!out || n_layers <= 0 || n_layers > 4096 || t_max <= 0 || t_max > (1 << 20))
+        return fail(QE_ERR_ARG, "qe_moe_create: bad argument (n_layers=%d t_max=%d)", n_layers, t_max);
+    *out = nullptr;
+    HIP_TRY(hipSetDevice(device));
+    qe_moe_ctx *c = new qe_moe_ctx();
+    c->device = device;
+    c->n_layers = n_layers;
+    c->t_max = t_max;
+    c->has_bias.assign(n_layers, 0);
+    c->ready.assign(n_layers, 0);
+    const size_t L = (size_t)n_layers, T = (size_t)t_max, NP = T * QE_K_USED;
+    const size_t max_items = NP / QE_LARGE_TC + QE_N_EXPERT;
+    const size_t nch = (NP + 1023) / 1024;
+    int rc = QE_OK;
+    QeScratch &S = c->S;
+#define A(ptr, bytes) \
+    if (rc == QE_OK) rc = dalloc(c, (void **)&(ptr), (bytes))
+    A(c->arena, L * QE_LAYER_EXPERT_BYTES);
+    A(c->router, L * QE_ROUTER_BYTES);
+    A(c->bias, L * QE_N_EXPERT * 4);
+    A(c->sh_gu, L * QE_SH_GU_BYTES);
+    A(c->sh_dn, L * QE_SH_DN_BYTES);
+    A(c->post_norm, L * QE_D * 4);
+    A(S.xn, T * QE_D * 4);
+    A(S.xq, T * QE_D);
+    A(S.xs, T * (QE_D / 32) * 4);
+    A(S.logits, T * QE_ROUTER_ROWS * 4);
+    A(S.shgu, T * QE_SH_GU_ROWS * 4);
+    A(S.ids, NP * 4);
+    A(S.wts, NP * 4);
+    A(S.shg, T * 4);
+    A(S.off, (QE_N_EXPERT + 1) * 4);
+    A(S.pairs, NP * 4);
+    A(S.items, max_items * sizeof(int4));
+    A(S.n_items, 4);
+    A(S.h, NP * QE_FF_EXP * 4);
+    A(S.hq, NP * QE_FF_EXP);
+    A(S.hs, NP * (QE_FF_EXP / 32) * 4);
+    A(S.sd, T * QE_D * 4);
+    A(S.yp, NP * QE_D * 4);
+    A(S.chunk_hist, nch * QE_N_EXPERT * 4);
+    A(S.counter, 256);
+    A(c->pingpong[0], T * QE_D * 4);
+    A(c->pingpong[1], T * QE_D * 4);
+#undef A
+    if (rc != QE_OK) {
+        free_all(c);
+        delete c;
+        return rc;
+    }
+    S.t_max = t_max;
+    S.prof = &c->prof;
+    if (hipMemset(S.counter, 0, 256) != hipSuccess || hipMemset(c->bias, 0, L * QE_N_EXPERT * 4) != hipSuccess ||
+        hipDeviceSynchronize() != hipSuccess) {
+        free_all(c);
+        delete c;
+        return fail(QE_ERR_HIP, "qe_moe_create: initial memset failed");
+    }
+    *out = c;
+    return QE_OK;
+}
+
+int qe_moe_destroy(qe_moe_ctx *c) {
+    if (!c) return QE_OK;
+    (void)hipSetDevice(c->device);
+    (void)hipDeviceSynchronize();
+    for (int i = 0; i < 2 * c->prof.cap; ++i) (void)hipEventDestroy(c->prof.ev[i]);
+    delete[] c->prof.ev;
+    delete[] c->prof.kid;
+    free_all(c);
+    delete c;
+    return QE_OK;
+}
+
+int qe_moe_upload_experts(qe_moe_ctx *c, int layer, int first, int n, const void *src, int on_dev, void *stream) {
+    if (!c || !src || layer < 0 || layer >= c->n_layers || first < 0 || n <= 0 || first + n > QE_N_EXPERT)
+        return fail(QE_ERR_ARG, "qe_moe_upload_experts: bad argument");
+    HIP_TRY(hipSetDevice(c->device));
+    uint8_t *dst = c->arena + (size_t)layer * QE_LAYER_EXPERT_BYTES + (size_t)first * QE_EXPERT_BYTES;
+    HIP_TRY(hipMemcpyAsync(dst, src, (size_t)n * QE_EXPERT_BYTES, on_dev ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice,
+                           (hipStream_t)stream));
+    return QE_OK;
+}
+
+int qe_moe_set_dense(qe_moe_ctx *c, int layer, const float *post_norm, const float *router, const float *bias,
+                     const void *sh_gu, const void *sh_down, int on_dev, void *stream) {
+    if (!c || layer < 0 || layer >= c->n_layers) return fail(QE_ERR_ARG, "qe_moe_set_dense: bad argument");
+    HIP_TRY(hipSetDevice(c->device));
+    const hipMemcpyKind k = on_dev ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice;
+    hipStream_t s = (hipStream_t)stream;
+    const QeLayerPtrs L = layer_ptrs(c, layer);
+    if (post_norm) HIP_TRY(hipMemcpyAsync((void *)L.post_norm, post_norm, QE_D * 4, k, s));
+    if (router) HIP_TRY(hipMemcpyAsync((void *)L.router, router, QE_ROUTER_BYTES, k, s));
+    if (bias) {
+        HIP_TRY(hipMemcpyAsync(c->bias + (size_t)layer * QE_N_EXPERT, bias, QE_N_EXPERT * 4, k, s));
+        c->has_bias[layer] = 1;
+    }
+    if (sh_gu) HIP_TRY(hipMemcpyAsync((void *)L.sh_gu, sh_gu, QE_SH_GU_BYTES, k, s));
+    if (sh_down) HIP_TRY(hipMemcpyAsync((void *)L.sh_dn, sh_down, QE_SH_DN_BYTES, k, s));
+    if (!on_dev) HIP_TRY(hipStreamSynchronize(s)); /* host sources need not outlive the call */
+    c->ready[layer] = 1;
+    return QE_OK;
+}
+
+static int check_fwd(qe_moe_ctx *c, int layer, const void *in, const void *out, int T) {
+    if (!c || !in || !out || T <= 0) return fail(QE_ERR_ARG, "forward: bad argument");
+    if (layer < 0 || layer >= c->n_layers) return fail(QE_ERR_ARG, "forward: layer %d out of range", layer);
+    if (T > c->t_max) return fail(QE_ERR_ARG, "forward: T=%d exceeds t_max=%d", T, c->t_max);
+    if (!c->ready[layer]) return fail(QE_ERR_STATE, "forward: layer %d has no dense weights", layer);
+    if (in == out) return fail(QE_ERR_ARG, "forward: output may not alias the input");
+    return QE_OK;
+}
+
+int qe_moe_forward(qe_moe_ctx *c, int layer, const float *x2, float *x, int T, void *stream) {
+    int rc = check_fwd(c, layer, x2, x, T);
+    if (rc) return rc;
+    HIP_TRY(hipSetDevice(c->device));
+    HIP_TRY(qe_launch_layer(layer_ptrs(c, layer), c->S, x2, true, x2, x, T, (hipStream_t)stream));
+    return QE_OK;
+}
+
+int qe_moe_forward_normed(qe_moe_ctx *c, int layer, const float *xn, float *y, int T, void *stream) {
+    int rc = check_fwd(c, layer, xn, y, T);
+    if (rc) return rc;
+    HIP_TRY(hipSetDevice(c->device));
+    HIP_TRY(qe_launch_layer(layer_ptrs(c, layer), c->S, xn, false, nullptr, y, T, (hipStream_t)stream));
+    return QE_OK;
+}
+
+int qe_moe_forward_stack(qe_moe_ctx *c, int first, int n, const float *x_in, float *x_out, int T, void *stream) {
+    if (!c || n <= 0 || first < 0 || first + n > c->n_layers)
+        return fail(QE_ERR_ARG, "forward_stack: bad layer range");
+    if (x_in == x_out) return fail(QE_ERR_ARG, "forward_stack: output may not alias the input");
+    const float *cur = x_in;
+    for (int i = 0; i < n; ++i) {
+        float *dst = (i == n - 1) ? x_out : c->pingpong[i & 1];
+        int rc = qe_moe_forward(c, first + i, cur, dst, T, stream);
+        if (rc) return rc;
+        cur = dst;
+    }
+    return QE_OK;
+}
+
+int qe_moe_get_routing(qe_moe_ctx *c, int T, int32_t *ids, float *wts, float *shg, int32_t *off, int32_t *pairs,
+                       float *shared_out, void *stream) {
+    if (!c || T <= 0 || T > c->t_max) return fail(QE_ERR_ARG, "get_routing: bad argument");
+    HIP_TRY(hipSetDevice(c->device));
+    hipStream_t s = (hipStream_t)stream;
+    const size_t np = (size_t)T * QE_K_USED;
+    if (ids) HIP_TRY(hipMemcpyAsync(ids, c->S.ids, np * 4, hipMemcpyDeviceToHost, s));
+    if (wts) HIP_TRY(hipMemcpyAsync(wts, c->S.wts, np * 4, hipMemcpyDeviceToHost, s));
+    if (shg) HIP_TRY(hipMemcpyAsync(shg, c->S.shg, (size_t)T * 4, hipMemcpyDeviceToHost, s));
+    if (off) HIP_TRY(hipMemcpyAsync(off, c->S.off, (QE_N_EXPERT + 1) * 4, hipMemcpyDeviceToHost, s));
+    if (pairs) HIP_TRY(hipMemcpyAsync(pairs, c->S.pairs, np * 4, hipMemcpyDeviceToHost, s));
+    if (shared_out) HIP_TRY(hipMemcpyAsync(shared_out, c->S.sd, (size_t)T * QE_D * 4, hipMemcpyDeviceToHost, s));
+    HIP_TRY(hipStreamSynchronize(s));
+    return QE_OK;
+}
+
+int qe_moe_dispatch(qe_moe_ctx *c, const int32_t *ids, int T, void *stream) {
+    if (!c || !ids || T <= 0 || T > c->t_max) return fail(QE_ERR_ARG, "dispatch: bad argument");
+    HIP_TRY(hipSetDevice(c->device));
+    HIP_TRY(hipMemcpyAsync(c->S.ids, ids, (size_t)T * QE_K_USED * 4, hipMemcpyDeviceToDevice, (hipStream_t)stream));
+    HIP_TRY(qe_launch_dispatch(c->S, T, (hipStream_t)stream));
+    return QE_OK;
+}
+
+int qe_moe_get_logits(qe_moe_ctx *c, int T, float *logits, void *stream) {
+    if (!c || !logits || T <= 0 || T > c->t_max) return fail(QE_ERR_ARG, "get_logits: bad argument");
+    HIP_TRY(hipSetDevice(c->device));
+    HIP_TRY(hipMemcpyAsync(logits, c->S.logits, (size_t)T * QE_ROUTER_ROWS * 4, hipMemcpyDeviceToHost, (hipStream_t)stream));
+    HIP_TRY(hipStreamSynchronize((hipStream_t)stream));
+    return QE_OK;
+}
+
+static const char *const k_prof_names[QP_N] = {
+    "k_route_small", "k_gu", "k_down_small", "k_normq", "k_gemm_canon<router>", "k_gemm_canon<shared_gu>",
+    "k_topk", "k_disp_hist+k_disp_scatter", "k_hquant", "k_down_large", "k_gemm_canon<shared_down>", "k_combine"};
+
+int qe_moe_profile(qe_moe_ctx *c, int enable) {
+    if (!c) return fail(QE_ERR_ARG, "profile: bad argument");
+    HIP_TRY(hipSetDevice(c->device));
+    QeProf &p = c->prof;
+    if (enable && !p.ev) {
+        p.cap = 8192;
+        p.ev = new hipEvent_t[2 * p.cap];
+        p.kid = new int[p.cap];
+        for (int i = 0; i < 2 * p.cap; ++i) HIP_TRY(hipEventCreate(&p.ev[i]));
+    }
+    p.on = enable != 0;
+    p.used = 0;
+    p.dropped = 0;
+    return QE_OK;
+}
+
+int qe_moe_profile_read(qe_moe_ctx *c, double *ms, int *launches, int n) {
+    if (!c || !ms || !launches || n < QP_N) return fail(QE_ERR_ARG, "profile_read: need arrays of %d", (int)QP_N);
+    HIP_TRY(hipSetDevice(c->device));
+    for (int k = 0; k < n; ++k) { ms[k] = 0.0; launches[k] = 0; }
+    QeProf &p = c->prof;
+    for (int i = 0; i < p.used; ++i) {
+        HIP_TRY(hipEventSynchronize(p.ev[2 * i + 1]));
+        float t = 0.f;
+        HIP_TRY(hipEventElapsedTime(&t, p.ev[2 * i], p.ev[2 * i + 1]));
+        ms[p.kid[i]] += t;
+        launches[p.kid[i]] += 1;
+    }
+    const int dropped = p.dropped;
+    p.used = 0;
+    p.dropped = 0;
+    if (dropped) return fail(QE_ERR_STATE, "profile_read: %d launches not recorded (event pool full)", dropped);
+    return QE_OK;
+}
+
+const char *qe_moe_profile_name(int id) { return (id >= 0 && id < QP_N) ? k_prof_names[id] : ""; }
+
+int qe_moe_arena_ptr(qe_moe_ctx *c, int layer, void **dev) {
+    if (!c || !dev || layer < 0 || layer >= c->n_layers) return fail(QE_ERR_ARG, "arena_ptr: bad argument");
+    *dev = c->arena + (size_t)layer * QE_LAYER_EXPERT_BYTES;
+    return QE_OK;
+}
+
+int qe_moe_synth_layer(qe_moe_ctx *c, int layer, uint64_t seed, const float *bias, void *stream) {
+    if (!c || layer < 0 || layer >= c->n_layers) return fail(QE_ERR_ARG, "synth_layer: bad argument");
+    HIP_TRY(hipSetDevice(c->device));
+    const QeLayerPtrs L = layer_ptrs(c, layer);
+    HIP_TRY(qe_launch_synth_layer((uint8_t *)L.arena, (float *)L.router, (uint8_t *)L.sh_gu, (uint8_t *)L.sh_dn,
+                                  (float *)L.post_norm, seed, layer, (hipStream_t)stream));
+    if (bias) {
+        HIP_TRY(hipMemcpyAsync(c->bias + (size_t)layer * QE_N_EXPERT, bias, QE_N_EXPERT * 4, hipMemcpyHostToDevice,
+                               (hipStream_t)stream));
+        HIP_TRY(hipStreamSynchronize((hipStream_t)stream));
+        c->has_bias[layer] = 1;
+    } else {
+        c->has_bias[layer] = 0;
+    }
+    c->ready[layer] = 1;
+    return QE_OK;
+}
+
+int qe_moe_synth_x(uint64_t seed, int inst, float *dev_out, int64_t n, void *stream) {
+    if (!dev_out || n < 0) return fail(QE_ERR_ARG, "synth_x: bad argument");
+    if (n == 0) return QE_OK;
+    HIP_TRY(qe_launch_synth_x(dev_out, seed, inst, n, (hipStream_t)stream));
+    return QE_OK;
+}
+
+}  // extern "C"

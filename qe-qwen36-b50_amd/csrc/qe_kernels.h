@@ -1,0 +1,81 @@
+// Kernel argument blocks and host launchers of the MoE block (internal).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "qe_device.h"
+
+#define QE_SMALL_T 8   /* tokens per call handled by the 3-launch small-T plan */
+#define QE_LARGE_TC 16 /* pairs per work item in the large-T plan */
+
+enum { GEMM_ROUTER = 0, GEMM_SHGU = 1, GEMM_SHDN = 2 };
+
+// One layer's weights inside the context.
+struct QeLayerPtrs {
+    const uint8_t *arena;     // 256 expert blobs
+    const float *router;      // [257][2048]
+    const float *bias;        // [256] or nullptr
+    const uint8_t *sh_gu;     // Q8 [1024][2048]
+    const uint8_t *sh_dn;     // Q8 [2048][512]
+    const float *post_norm;   // [2048]
+};
+
+// Optional per-kernel event timing (host side): when `on`, every launch of
+// qe_launch_layer is bracketed by two events on its stream.
+enum { QP_ROUTE_SMALL, QP_GU, QP_DOWN_SMALL, QP_NORMQ, QP_ROUTER, QP_SHGU, QP_TOPK, QP_DISPATCH, QP_HQUANT,
+       QP_DOWN_LARGE, QP_SHDN, QP_COMBINE, QP_N };
+struct QeProf {
+    bool on = false;
+    int used = 0, cap = 0, dropped = 0;
+    hipEvent_t *ev = nullptr; // 2*cap events
+    int *kid = nullptr;       // kernel id per pair
+};
+
+// Scratch of a context, sized for t_max tokens.
+struct QeScratch {
+    float *xn; int8_t *xq; float *xs;       // [T][2048], [T][2048], [T][64]
+    float *logits;                          // [T][257]
+    float *shgu;                            // [T][1024]
+    int32_t *ids; float *wts; float *shg;   // [T][8], [T][8], [T]
+    int32_t *off; int32_t *pairs;           // [257], [T*8]
+    int4 *items; int32_t *n_items;          // work items (expert, first pair, count)
+    float *h; int8_t *hq; float *hs;        // [T*8][512], [T*8][512], [T*8][16]
+    float *sd;                              // [T][2048] shared-expert output
+    float *yp;                              // [T*8][2048] weighted expert outputs
+    int32_t *chunk_hist;                    // [T*8/1024][256]
+    uint32_t *counter;                      // last-block ticket (self-resetting)
+    int t_max;
+    QeProf *prof;                           // host-side timing, may be nullptr
+};
+
+struct QeRouteArgs {
+    const float *x; int T; const float *post_norm;
+    const float *router; const float *bias; const uint8_t *sh_gu;
+    float *xn; int8_t *xq; float *xs; float *logits; float *shgu;
+    int32_t *ids; float *wts; float *shg; int32_t *off; int32_t *pairs; int4 *items; int32_t *n_items;
+    uint32_t *counter;
+};
+struct QeExpertArgs {
+    const uint8_t *arena; const int8_t *xq; const float *xs;
+    const int32_t *pairs; const int4 *items; const int32_t *n_items;
+    float *h;
+};
+struct QeDownArgs {
+    const uint8_t *arena; const uint8_t *sh_dn; int T;
+    const float *h; const int8_t *hq; const float *hs; const float *shgu;
+    const int32_t *pairs; const int4 *items; const int32_t *n_items;
+    const float *wts; const float *shg; const float *x2;
+    float *yp; float *sd; float *out;
+};
+struct QeGemmArgs {
+    const float *A; int T; const float *Bf; const uint8_t *Bq; const float *bias; float *C;
+};
+
+// Launchers (qe_kernels.hip).  xin: layer input; post_norm: nullptr = input is
+// already normalised; x2: residual added to the output or nullptr.
+hipError_t qe_launch_layer(const QeLayerPtrs &L, const QeScratch &S, const float *xin, bool norm, const float *x2,
+                           float *out, int T, hipStream_t st);
+hipError_t qe_launch_dispatch(const QeScratch &S, int T, hipStream_t st);
+hipError_t qe_launch_synth_layer(uint8_t *arena_l, float *router_l, uint8_t *sh_gu_l, uint8_t *sh_dn_l,
+                                 float *post_norm_l, uint64_t seed, int layer, hipStream_t st);
+hipError_t qe_launch_synth_x(float *out, uint64_t seed, int inst, int64_t n, hipStream_t st);

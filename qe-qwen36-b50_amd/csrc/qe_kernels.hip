@@ -1,0 +1,786 @@
+// MoE block kernels for gfx950 (wave64).
+//
+// Two launch plans share these kernels (host side in qe_api.hip):
+//  * small T (<= QE_SMALL_T tokens: B=1 decode and the batched verify of
+//    decode_multi<NT>, engine/qe.cpp:1653-1737, 2466-2572): three launches,
+//      k_route_small  norm + router + shared gate|up + (last block) top-8 + dispatch
+//      k_gu           routed gate/up + SwiGLU, weight rows read once per expert
+//      k_down_small   h quantisation + routed down + shared down + combine
+//  * large T (prefill, Engine::moe_batched, engine/qe.cpp:1957-2047):
+//      k_normq, k_gemm_canon (router / shared), k_topk, k_disp_hist,
+//      k_disp_scatter, k_gu, k_hquant, k_down_large, k_combine.
+// Routing (RMSNorm, router dot products, top-8) follows the checker's
+// canonical fp32 order exactly; expert products use exact int8 block dots
+// with fp32 block scaling, so they agree with the CPU path to fp32 rounding.
+#include "qe_kernels.h"
+
+// ===========================================================================
+// top-8 of one token by one wave (engine/qe.cpp:1454-1483 semantics):
+// maximum logit first; ties go to the smaller (e % 16, e / 16), the order the
+// reference's 16-lane reduction produces.  Lane l holds e = l + 64 j.
+// ===========================================================================
+QE_DEV void wave_topk(const float *lg, int lane, int32_t *ids, float *wts, float *shg, int *lds_ids = nullptr) {
+    float v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = lg[lane + 64 * j];
+    float sel[QE_K_USED];
+    int id[QE_K_USED];
+#pragma unroll
+    for (int k = 0; k < QE_K_USED; ++k) {
+        float bv = -INFINITY;
+        int bk = 1 << 20, be = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int e = lane + 64 * j, key = (e & 15) * 16 + (e >> 4);
+            if (v[j] > bv || (v[j] == bv && key < bk)) { bv = v[j]; bk = key; be = e; }
+        }
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const float ov = __shfl_xor(bv, off, 64);
+            const int ok = __shfl_xor(bk, off, 64), oe = __shfl_xor(be, off, 64);
+            if (ov > bv || (ov == bv && ok < bk)) { bv = ov; bk = ok; be = oe; }
+        }
+        sel[k] = bv;
+        id[k] = be;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            if (lane + 64 * j == be) v[j] = -INFINITY;
+    }
+    if (lane == 0) {
+        float s = 0.f;
+#pragma unroll
+        for (int k = 0; k < QE_K_USED; ++k) s += expf(sel[k] - sel[0]);
+#pragma unroll
+        for (int k = 0; k < QE_K_USED; ++k) {
+            ids[k] = id[k];
+            if (lds_ids) lds_ids[k] = id[k];
+            wts[k] = expf(sel[k] - sel[0]) / s;
+        }
+        *shg = 1.f / (1.f + expf(-lg[QE_N_EXPERT]));
+    }
+}
+
+// Exclusive scan of one int per thread over a 256-thread block; returns the
+// exclusive prefix, *total gets the sum.  `tmp` is 256 ints of LDS.
+QE_DEV int block_scan256(int v, int *tmp, int *total) {
+    const int tid = threadIdx.x;
+    tmp[tid] = v;
+    __syncthreads();
+#pragma unroll
+    for (int off = 1; off < 256; off <<= 1) {
+        const int a = tid >= off ? tmp[tid - off] : 0;
+        __syncthreads();
+        tmp[tid] += a;
+        __syncthreads();
+    }
+    const int incl = tmp[tid];
+    *total = tmp[255];
+    __syncthreads();
+    return incl - v;
+}
+
+// One canonical normalisation of a 2048-vector by one wave.  Lane c owns the
+// 32 contiguous elements [32c, 32c+32) in v[]; on return v holds xn.
+QE_DEV void wave_norm_chunk(float v[32], const float *post_norm, int lane) {
+    if (!post_norm) return;
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) ss = fmaf(v[i], v[i], ss);
+    ss = wave_sum_canon(ss);
+    const float inv = 1.0f / sqrtf(ss / (float)QE_D + QE_RMS_EPS);
+    const float4 *wr = (const float4 *)(post_norm + lane * 32);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float4 w = wr[i];
+        v[4 * i + 0] = (v[4 * i + 0] * inv) * w.x;
+        v[4 * i + 1] = (v[4 * i + 1] * inv) * w.y;
+        v[4 * i + 2] = (v[4 * i + 2] * inv) * w.z;
+        v[4 * i + 3] = (v[4 * i + 3] * inv) * w.w;
+    }
+}
+
+// Quantise the 32 values a lane holds (one block) and store int8 + scale.
+QE_DEV void lane_quant_store(const float v[32], int8_t *q_out, float *s_out) {
+    float amax = 0.f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
+    float d;
+    const float id = quant_scale_inv(amax, d);
+    uint32_t w[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        uint32_t x = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) x |= (uint32_t)(uint8_t)quant_one(v[4 * i + j], id) << (8 * j);
+        w[i] = x;
+    }
+    ((uint4 *)q_out)[0] = make_uint4(w[0], w[1], w[2], w[3]);
+    ((uint4 *)q_out)[1] = make_uint4(w[4], w[5], w[6], w[7]);
+    *s_out = d;
+}
+
+QE_DEV void load32(const float *p, float v[32]) {
+    const float4 *q = (const float4 *)p;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float4 t = q[i];
+        v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w;
+    }
+}
+QE_DEV void unpack_i8x32(uint4 a, uint4 b, float w[32]) {
+    const uint32_t d[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) w[4 * i + j] = (float)(int8_t)((d[i] >> (8 * j)) & 0xff);
+}
+
+// ===========================================================================
+// small T, launch 1: norm + router + shared gate|up; the last block to finish
+// does top-8 and the dispatch for all T tokens.
+// grid = ceil((257 + 1024) / 4), block = 256: one wave per weight row.
+// ===========================================================================
+__global__ __launch_bounds__(256) void k_route_small(QeRouteArgs a) {
+    __shared__ float sx[QE_SMALL_T * QE_D]; // sx[t][i][c] = xn[t][32c + i]
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, T = a.T;
+
+    for (int t = wv; t < T; t += 4) {
+        float v[32];
+        load32(a.x + (size_t)t * QE_D + lane * 32, v);
+        wave_norm_chunk(v, a.post_norm, lane);
+#pragma unroll
+        for (int i = 0; i < 32; ++i) sx[t * QE_D + i * 64 + lane] = v[i];
+        if ((int)blockIdx.x == t) {
+            float4 *xo = (float4 *)(a.xn + (size_t)t * QE_D + lane * 32);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) xo[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+            lane_quant_store(v, a.xq + (size_t)t * QE_D + lane * 32, a.xs + (size_t)t * (QE_D / 32) + lane);
+        }
+    }
+    __syncthreads();
+
+    const int row = blockIdx.x * 4 + wv;
+    if (row < QE_ROUTER_ROWS) {
+        float w[32];
+        load32(a.router + (size_t)row * QE_D + lane * 32, w);
+        const bool add_bias = a.bias && row < QE_N_EXPERT;
+        const float b = add_bias ? a.bias[row] : 0.f;
+        for (int t = 0; t < T; ++t) {
+            float acc = 0.f;
+#pragma unroll
+            for (int i = 0; i < 32; ++i) acc = fmaf(w[i], sx[t * QE_D + i * 64 + lane], acc);
+            acc = wave_sum_canon(acc);
+            if (lane == 0) a.logits[t * QE_ROUTER_ROWS + row] = add_bias ? acc + b : acc;
+        }
+    } else if (row < QE_ROUTER_ROWS + QE_SH_GU_ROWS) {
+        const int r = row - QE_ROUTER_ROWS;
+        const uint8_t *rp = a.sh_gu + (size_t)r * QE_SH_GU_ROW_BYTES;
+        const uint4 q0 = ((const uint4 *)(rp + lane * 32))[0], q1 = ((const uint4 *)(rp + lane * 32))[1];
+        const float sc = f16_bits_to_f32(((const uint16_t *)(rp + QE_D))[lane]);
+        float w[32];
+        unpack_i8x32(q0, q1, w);
+        for (int t = 0; t < T; ++t) {
+            float acc = 0.f;
+#pragma unroll
+            for (int i = 0; i < 32; ++i) acc = fmaf(w[i], sx[t * QE_D + i * 64 + lane], acc);
+            acc = wave_sum_canon(acc * sc);
+            if (lane == 0) a.shgu[t * QE_SH_GU_ROWS + r] = acc;
+        }
+    }
+
+    // ---- last block: top-8 + dispatch ----
+    __threadfence();
+    __syncthreads();
+    int *si = (int *)sx; // reuse LDS
+    if (threadIdx.x == 0) si[0] = (int)atomicAdd(a.counter, 1u);
+    __syncthreads();
+    const bool last = si[0] == (int)gridDim.x - 1;
+    __syncthreads();
+    if (!last) return;
+    __threadfence();
+    int *s_ids = si, *s_scan = si + 64, *s_off = si + 64 + 256;
+    for (int t = wv; t < T; t += 4)
+        wave_topk(a.logits + t * QE_ROUTER_ROWS, lane, a.ids + t * QE_K_USED, a.wts + t * QE_K_USED, a.shg + t,
+                  s_ids + t * QE_K_USED);
+    __syncthreads();
+    const int np = T * QE_K_USED, tid = threadIdx.x;
+    int cnt = 0;
+    for (int p = 0; p < np; ++p) cnt += s_ids[p] == tid;
+    int total;
+    const int off = block_scan256(cnt, s_scan, &total);
+    s_off[tid] = off;
+    a.off[tid] = off;
+    if (tid == 0) a.off[QE_N_EXPERT] = total;
+    int nitems;
+    const int item = block_scan256(cnt > 0 ? 1 : 0, s_scan, &nitems);
+    if (cnt > 0) a.items[item] = make_int4(tid, off, cnt, 0);
+    if (tid == 0) *a.n_items = nitems;
+    __syncthreads();
+    if (tid < np) {
+        const int e = s_ids[tid];
+        int rank = 0;
+        for (int p = 0; p < tid; ++p) rank += s_ids[p] == e;
+        a.pairs[s_off[e] + rank] = tid;
+    }
+    if (tid == 0) atomicExch(a.counter, 0u);
+}
+
+// ===========================================================================
+// routed gate/up + SwiGLU for one work item (expert e, up to TC of its pairs)
+// and 16 rows.  grid = (items, 32 row groups), block = 256 (4 waves x 4 rows;
+// 16 lanes per row, lane owns blocks l16 + 16 j).  Weight rows are read and
+// decoded once, then dotted with every token of the item.
+// h[p][r] = silu(g) * u in fp32 (engine/qe.cpp:2066-2072).
+// ===========================================================================
+template <int TC>
+__global__ __launch_bounds__(256) void k_gu(QeExpertArgs a) {
+    __shared__ uint4 sxq[TC * QE_D / 16];
+    __shared__ float sxs[TC * (QE_D / 32)];
+    __shared__ int sp[TC];
+    if ((int)blockIdx.x >= *a.n_items) return;
+    const int4 it = a.items[blockIdx.x];
+    const int e = it.x, start = it.y, n = it.z, tid = threadIdx.x;
+    if (tid < n) sp[tid] = a.pairs[start + tid];
+    __syncthreads();
+    for (int i = tid; i < n * (QE_D / 16); i += 256) {
+        const int j = i / (QE_D / 16), part = i % (QE_D / 16);
+        sxq[i] = ((const uint4 *)(a.xq + (size_t)(sp[j] / QE_K_USED) * QE_D))[part];
+    }
+    for (int i = tid; i < n * (QE_D / 32); i += 256) {
+        const int j = i / (QE_D / 32), b = i % (QE_D / 32);
+        sxs[i] = a.xs[(size_t)(sp[j] / QE_K_USED) * (QE_D / 32) + b];
+    }
+    const int lane = tid & 63, wv = tid >> 6, l16 = lane & 15;
+    const int r = blockIdx.y * 16 + wv * 4 + (lane >> 4);
+    const uint8_t *base = a.arena + (size_t)e * QE_EXPERT_BYTES;
+    const uint8_t *rg = base + (size_t)r * QE_GU_ROW_BYTES, *ru = base + (size_t)(QE_FF_EXP + r) * QE_GU_ROW_BYTES;
+    nl4_blk dg[4], du[4];
+    float sg[4], su[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int b = l16 + 16 * j;
+        dg[j] = nl4_decode_block(*(const uint4 *)(rg + b * 16));
+        du[j] = nl4_decode_block(*(const uint4 *)(ru + b * 16));
+        sg[j] = f16_bits_to_f32(((const uint16_t *)(rg + QE_D / 2))[b]);
+        su[j] = f16_bits_to_f32(((const uint16_t *)(ru + QE_D / 2))[b]);
+    }
+    __syncthreads();
+    for (int j = 0; j < n; ++j) {
+        float G = 0.f, U = 0.f;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int b = l16 + 16 * q;
+            const uint4 x0 = sxq[j * (QE_D / 16) + b * 2], x1 = sxq[j * (QE_D / 16) + b * 2 + 1];
+            const float xsv = sxs[j * (QE_D / 32) + b];
+            G = fmaf(sg[q] * xsv, (float)nl4_block_dot(dg[q], x0, x1), G);
+            U = fmaf(su[q] * xsv, (float)nl4_block_dot(du[q], x0, x1), U);
+        }
+        G = sum16(G);
+        U = sum16(U);
+        if (l16 == 0) a.h[(size_t)sp[j] * QE_FF_EXP + r] = silu_mul(G, U);
+    }
+}
+
+// ===========================================================================
+// small T, launch 3: quantise h of every pair, routed down + weight, shared
+// expert down on silu(g)*u, combine (engine/qe.cpp:2033-2045 order:
+// x2 + shg*sd, then + y_{t,k} for k = 0..7).  grid = 2048/8, block = 128
+// (2 waves x 4 rows, 16 lanes per row, lane = block of the 512-wide row).
+// ===========================================================================
+__global__ __launch_bounds__(128) void k_down_small(QeDownArgs a) {
+    __shared__ uint4 shq[QE_SMALL_T * QE_K_USED * QE_FF_EXP / 16];
+    __shared__ float shs[QE_SMALL_T * QE_K_USED * (QE_FF_EXP / 32)];
+    __shared__ float shh[QE_SMALL_T * QE_FF_SH];
+    __shared__ float syp[QE_SMALL_T * QE_K_USED * 8];
+    const int T = a.T, np = T * QE_K_USED, tid = threadIdx.x;
+    for (int i = tid; i < np * (QE_FF_EXP / 32); i += 128) {
+        const int p = i / (QE_FF_EXP / 32), b = i % (QE_FF_EXP / 32);
+        float v[32];
+        load32(a.h + (size_t)p * QE_FF_EXP + b * 32, v);
+        lane_quant_store(v, (int8_t *)shq + p * QE_FF_EXP + b * 32, shs + i);
+    }
+    for (int i = tid; i < T * QE_FF_SH; i += 128) {
+        const int t = i / QE_FF_SH, k = i % QE_FF_SH;
+        shh[i] = silu_mul(a.shgu[t * QE_SH_GU_ROWS + k], a.shgu[t * QE_SH_GU_ROWS + QE_FF_SH + k]);
+    }
+    __syncthreads();
+    const int lane = tid & 63, wv = tid >> 6, l16 = lane & 15, rl = wv * 4 + (lane >> 4);
+    const int r = blockIdx.x * 8 + rl;
+    const int nitems = *a.n_items;
+    for (int i = 0; i < nitems; ++i) {
+        const int4 it = a.items[i];
+        const uint8_t *drow = a.arena + (size_t)it.x * QE_EXPERT_BYTES + QE_EXPERT_DOWN_OFF + (size_t)r * QE_DN_ROW_BYTES;
+        const nl4_blk w = nl4_decode_block(*(const uint4 *)(drow + l16 * 16));
+        const float sc = f16_bits_to_f32(((const uint16_t *)(drow + QE_FF_EXP / 2))[l16]);
+        for (int j = 0; j < it.z; ++j) {
+            const int p = a.pairs[it.y + j];
+            const int P = nl4_block_dot(w, shq[p * (QE_FF_EXP / 16) + l16 * 2], shq[p * (QE_FF_EXP / 16) + l16 * 2 + 1]);
+            float v = (sc * shs[p * (QE_FF_EXP / 32) + l16]) * (float)P;
+            v = sum16(v);
+            if (l16 == 0) syp[p * 8 + rl] = a.wts[p] * v;
+        }
+    }
+    // shared down: Q8 row r, lane = block l16
+    const uint8_t *srow = a.sh_dn + (size_t)r * QE_SH_DN_ROW_BYTES;
+    float w8[32];
+    unpack_i8x32(((const uint4 *)(srow + l16 * 32))[0], ((const uint4 *)(srow + l16 * 32))[1], w8);
+    const float ssc = f16_bits_to_f32(((const uint16_t *)(srow + QE_FF_SH))[l16]);
+    float sdv[QE_SMALL_T];
+#pragma unroll
+    for (int t = 0; t < QE_SMALL_T; ++t) {
+        sdv[t] = 0.f;
+        if (t < T) {
+            float acc = 0.f;
+#pragma unroll
+            for (int i = 0; i < 32; ++i) acc = fmaf(w8[i], shh[t * QE_FF_SH + l16 * 32 + i], acc);
+            sdv[t] = sum16(acc * ssc);
+        }
+    }
+    __syncthreads();
+    if (l16 == 0) {
+#pragma unroll
+        for (int t = 0; t < QE_SMALL_T; ++t) {
+            if (t >= T) break;
+            const size_t o = (size_t)t * QE_D + r;
+            float acc = (a.x2 ? a.x2[o] : 0.f) + a.shg[t] * sdv[t];
+#pragma unroll
+            for (int k = 0; k < QE_K_USED; ++k) acc += syp[(t * QE_K_USED + k) * 8 + rl];
+            a.out[o] = acc;
+            a.sd[o] = sdv[t];
+        }
+    }
+}
+
+// ===========================================================================
+// large T kernels
+// ===========================================================================
+// wave per token: xn, xq, xs
+__global__ __launch_bounds__(256) void k_normq(const float *x, int T, const float *post_norm, float *xn, int8_t *xq,
+                                               float *xs) {
+    const int lane = threadIdx.x & 63, t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t >= T) return;
+    float v[32];
+    load32(x + (size_t)t * QE_D + lane * 32, v);
+    wave_norm_chunk(v, post_norm, lane);
+    float4 *xo = (float4 *)(xn + (size_t)t * QE_D + lane * 32);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) xo[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+    lane_quant_store(v, xq + (size_t)t * QE_D + lane * 32, xs + (size_t)t * (QE_D / 32) + lane);
+}
+
+// Tiled fp32 GEMM C[m][n] = sum_k A[m][k] B[n][k] in the canonical order:
+// per 32-wide k chunk an fma chain from 0, chunk sums merged by the pairwise
+// tree (chunks (c, c+1), then pairs of pairs, ...).  Tile 64 x 64, 256
+// threads, 4 x 4 outputs per thread.
+//   GEMM_ROUTER: A = xn [T][2048], B = fp32 rows [257][2048], C = logits (+ bias)
+//   GEMM_SHGU:   A = xn, B = Q8 rows [1024][2048], C = shgu [T][1024]
+//   GEMM_SHDN:   A = silu(g)*u from shgu, K = 512, B = Q8 rows [2048][512], C = sd
+template <int MODE>
+__global__ __launch_bounds__(256) void k_gemm_canon(QeGemmArgs a) {
+    constexpr int KD = MODE == GEMM_SHDN ? QE_FF_SH : QE_D;
+    constexpr int NCH = KD / 32;
+    constexpr int NROWS = MODE == GEMM_ROUTER ? QE_ROUTER_ROWS : (MODE == GEMM_SHGU ? QE_SH_GU_ROWS : QE_D);
+    __shared__ float As[32][68];
+    __shared__ float Bs[32][68];
+    const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+    const int m0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
+    const int lr = tid >> 2, lk = (tid & 3) * 8; // loader: row lr of the tile, 8 k values
+    float st[7][4][4];
+    for (int c = 0; c < NCH; ++c) {
+        // ---- load A tile: rows m0+lr, k = c*32 + lk .. +7, stored transposed ----
+        {
+            const int m = m0 + lr;
+            float v[8];
+            if (m < a.T) {
+                if (MODE == GEMM_SHDN) {
+                    const float *g = a.A + (size_t)m * QE_SH_GU_ROWS + c * 32 + lk;
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) v[i] = silu_mul(g[i], g[QE_FF_SH + i]);
+                } else {
+                    const float4 *p = (const float4 *)(a.A + (size_t)m * QE_D + c * 32 + lk);
+                    const float4 p0 = p[0], p1 = p[1];
+                    v[0] = p0.x; v[1] = p0.y; v[2] = p0.z; v[3] = p0.w; v[4] = p1.x; v[5] = p1.y; v[6] = p1.z; v[7] = p1.w;
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) v[i] = 0.f;
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) As[lk + i][lr] = v[i];
+        }
+        // ---- load B tile ----
+        {
+            const int n = n0 + lr;
+            float v[8];
+            if (n < NROWS) {
+                if (MODE == GEMM_ROUTER) {
+                    const float4 *p = (const float4 *)(a.Bf + (size_t)n * QE_D + c * 32 + lk);
+                    const float4 p0 = p[0], p1 = p[1];
+                    v[0] = p0.x; v[1] = p0.y; v[2] = p0.z; v[3] = p0.w; v[4] = p1.x; v[5] = p1.y; v[6] = p1.z; v[7] = p1.w;
+                } else {
+                    const size_t rb = (size_t)KD + KD / 32 * 2;
+                    const uint8_t *row = a.Bq + (size_t)n * rb;
+                    const uint2 q = *(const uint2 *)(row + c * 32 + lk);
+                    const float sc = f16_bits_to_f32(((const uint16_t *)(row + KD))[c]);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        v[i] = (float)(int8_t)((q.x >> (8 * i)) & 0xff) * sc;
+                        v[4 + i] = (float)(int8_t)((q.y >> (8 * i)) & 0xff) * sc;
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) v[i] = 0.f;
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) Bs[lk + i][lr] = v[i];
+        }
+        __syncthreads();
+        float acc[4][4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[i][j] = 0.f;
+#pragma unroll
+        for (int kk = 0; kk < 32; ++kk) {
+            const float4 av = *(const float4 *)&As[kk][ty * 4];
+            const float4 bv = *(const float4 *)&Bs[kk][tx * 4];
+            const float ar[4] = {av.x, av.y, av.z, av.w}, br[4] = {bv.x, bv.y, bv.z, bv.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(ar[i], br[j], acc[i][j]);
+        }
+        __syncthreads();
+        // ---- pairwise-tree merge of this chunk ----
+        bool carry = true;
+#pragma unroll
+        for (int l = 0; l < 7; ++l) {
+            if (carry) {
+                if (c & (1 << l)) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) acc[i][j] = st[l][i][j] + acc[i][j];
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) st[l][i][j] = acc[i][j];
+                    carry = false;
+                }
+            }
+        }
+    }
+    constexpr int LV = NCH == 64 ? 6 : (NCH == 16 ? 4 : -1);
+    static_assert(LV >= 0, "chunk count must be 16 or 64");
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int m = m0 + ty * 4 + i;
+        if (m >= a.T) continue;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int n = n0 + tx * 4 + j;
+            if (n >= NROWS) continue;
+            float v = st[LV][i][j];
+            if (MODE == GEMM_ROUTER && a.bias && n < QE_N_EXPERT) v = v + a.bias[n];
+            a.C[(size_t)m * NROWS + n] = v;
+        }
+    }
+}
+
+__global__ __launch_bounds__(256) void k_topk(const float *logits, int T, int32_t *ids, float *wts, float *shg) {
+    const int lane = threadIdx.x & 63, t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t >= T) return;
+    wave_topk(logits + (size_t)t * QE_ROUTER_ROWS, lane, ids + t * QE_K_USED, wts + t * QE_K_USED, shg + t);
+}
+
+// Dispatch pass 1: per-chunk (1024 pairs) expert histogram.
+__global__ __launch_bounds__(1024) void k_disp_hist(const int32_t *ids, int np, int32_t *chunk_hist) {
+    __shared__ int h[QE_N_EXPERT];
+    const int tid = threadIdx.x, p = blockIdx.x * 1024 + tid;
+    if (tid < QE_N_EXPERT) h[tid] = 0;
+    __syncthreads();
+    if (p < np) atomicAdd(&h[ids[p]], 1);
+    __syncthreads();
+    if (tid < QE_N_EXPERT) chunk_hist[blockIdx.x * QE_N_EXPERT + tid] = h[tid];
+}
+
+// Dispatch pass 2: offsets and the stable scatter (engine/qe.cpp:1968-1976).
+// Inside a chunk, a pair's rank among earlier same-expert pairs is the count
+// in earlier waves plus its rank in its own wave (8 ballots on the id bits).
+// Block 0 also writes off[] and the work items (expert, first pair, count <= TC).
+__global__ __launch_bounds__(1024) void k_disp_scatter(const int32_t *ids, int np, const int32_t *chunk_hist, int nch,
+                                                       int tc, int32_t *off_out, int32_t *pairs, int4 *items,
+                                                       int32_t *n_items) {
+    __shared__ int s_before[QE_N_EXPERT], s_off[QE_N_EXPERT], s_cnt[QE_N_EXPERT], s_scan[QE_N_EXPERT];
+    __shared__ int s_w[16][QE_N_EXPERT];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    for (int i = tid; i < 16 * QE_N_EXPERT; i += 1024) (&s_w[0][0])[i] = 0;
+    if (tid < QE_N_EXPERT) {
+        int tot = 0, bef = 0;
+        for (int c = 0; c < nch; ++c) {
+            const int v = chunk_hist[c * QE_N_EXPERT + tid];
+            if (c < (int)blockIdx.x) bef += v;
+            tot += v;
+        }
+        s_before[tid] = bef;
+        s_cnt[tid] = tot;
+    }
+    __syncthreads();
+    if (tid < 256) {
+        // exclusive scan of s_cnt over 256 experts (threads 0..255)
+        s_scan[tid] = s_cnt[tid];
+    }
+    __syncthreads();
+    for (int o = 1; o < 256; o <<= 1) {
+        int v = 0;
+        if (tid < 256 && tid >= o) v = s_scan[tid - o];
+        __syncthreads();
+        if (tid < 256) s_scan[tid] += v;
+        __syncthreads();
+    }
+    if (tid < 256) s_off[tid] = s_scan[tid] - s_cnt[tid];
+    __syncthreads();
+    if (blockIdx.x == 0) {
+        if (tid < 256) off_out[tid] = s_off[tid];
+        if (tid == 0) off_out[QE_N_EXPERT] = s_scan[255];
+        // work items: ceil(cnt/tc) per expert
+        __shared__ int s_ni[QE_N_EXPERT];
+        if (tid < 256) s_ni[tid] = (s_cnt[tid] + tc - 1) / tc;
+        __syncthreads();
+        for (int o = 1; o < 256; o <<= 1) {
+            int v = 0;
+            if (tid < 256 && tid >= o) v = s_ni[tid - o];
+            __syncthreads();
+            if (tid < 256) s_ni[tid] += v;
+            __syncthreads();
+        }
+        if (tid < 256) {
+            const int nie = (s_cnt[tid] + tc - 1) / tc, base = s_ni[tid] - nie;
+            for (int c = 0; c < nie; ++c)
+                items[base + c] = make_int4(tid, s_off[tid] + c * tc, min(tc, s_cnt[tid] - c * tc), 0);
+            if (tid == 255) *n_items = s_ni[255];
+        }
+    }
+    const int p = blockIdx.x * 1024 + tid;
+    const bool valid = p < np;
+    const int e = valid ? ids[p] : 0;
+    unsigned long long peers = __ballot(valid);
+#pragma unroll
+    for (int bit = 0; bit < 8; ++bit) {
+        const unsigned long long b = __ballot(valid && ((e >> bit) & 1));
+        peers &= ((e >> bit) & 1) ? b : ~b;
+    }
+    const unsigned long long lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    const int rank = __popcll(peers & lt);
+    if (valid && rank == 0) s_w[wv][e] = __popcll(peers);
+    __syncthreads();
+    if (valid) {
+        int cross = 0;
+        for (int w = 0; w < wv; ++w) cross += s_w[w][e];
+        pairs[s_off[e] + s_before[e] + cross + rank] = p;
+    }
+}
+
+// h -> per-32 int8 + fp32 scale, one thread per (pair, block).
+__global__ __launch_bounds__(256) void k_hquant(const float *h, int nblk, int8_t *hq, float *hs) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= nblk) return;
+    float v[32];
+    load32(h + (size_t)i * 32, v);
+    lane_quant_store(v, hq + (size_t)i * 32, hs + i);
+}
+
+// routed down for one item and 64 rows: yp[p][r] = w_p * dot(D_e[r], hq_p).
+// grid = (items, 2048/64), block = 256 (4 waves x 4 rows x 4 passes).
+template <int TC>
+__global__ __launch_bounds__(256) void k_down_large(QeDownArgs a) {
+    __shared__ uint4 shq[TC * QE_FF_EXP / 16];
+    __shared__ float shs[TC * (QE_FF_EXP / 32)];
+    __shared__ int sp[TC];
+    if ((int)blockIdx.x >= *a.n_items) return;
+    const int4 it = a.items[blockIdx.x];
+    const int n = it.z, tid = threadIdx.x;
+    if (tid < n) sp[tid] = a.pairs[it.y + tid];
+    __syncthreads();
+    for (int i = tid; i < n * (QE_FF_EXP / 16); i += 256) {
+        const int j = i / (QE_FF_EXP / 16), part = i % (QE_FF_EXP / 16);
+        shq[i] = ((const uint4 *)(a.hq + (size_t)sp[j] * QE_FF_EXP))[part];
+    }
+    for (int i = tid; i < n * (QE_FF_EXP / 32); i += 256) {
+        const int j = i / (QE_FF_EXP / 32), b = i % (QE_FF_EXP / 32);
+        shs[i] = a.hs[(size_t)sp[j] * (QE_FF_EXP / 32) + b];
+    }
+    __syncthreads();
+    const int lane = tid & 63, wv = tid >> 6, l16 = lane & 15;
+    const uint8_t *dbase = a.arena + (size_t)it.x * QE_EXPERT_BYTES + QE_EXPERT_DOWN_OFF;
+#pragma unroll 1
+    for (int pass = 0; pass < 4; ++pass) {
+        const int r = blockIdx.y * 64 + pass * 16 + wv * 4 + (lane >> 4);
+        const uint8_t *drow = dbase + (size_t)r * QE_DN_ROW_BYTES;
+        const nl4_blk w = nl4_decode_block(*(const uint4 *)(drow + l16 * 16));
+        const float sc = f16_bits_to_f32(((const uint16_t *)(drow + QE_FF_EXP / 2))[l16]);
+        for (int j = 0; j < n; ++j) {
+            const int P = nl4_block_dot(w, shq[j * (QE_FF_EXP / 16) + l16 * 2], shq[j * (QE_FF_EXP / 16) + l16 * 2 + 1]);
+            float v = (sc * shs[j * (QE_FF_EXP / 32) + l16]) * (float)P;
+            v = sum16(v);
+            if (l16 == 0) a.yp[(size_t)sp[j] * QE_D + r] = a.wts[sp[j]] * v;
+        }
+    }
+}
+
+// out[t][r] = x2 + shg*sd + sum_k yp[t*8+k][r]  (engine/qe.cpp:2036-2044)
+__global__ __launch_bounds__(256) void k_combine(QeDownArgs a) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (size_t)a.T * QE_D) return;
+    const int t = (int)(i / QE_D), r = (int)(i % QE_D);
+    float acc = (a.x2 ? a.x2[i] : 0.f) + a.shg[t] * a.sd[i];
+#pragma unroll
+    for (int k = 0; k < QE_K_USED; ++k) acc += a.yp[((size_t)t * QE_K_USED + k) * QE_D + r];
+    a.out[i] = acc;
+}
+
+// ===========================================================================
+// synthetic fills (one 8-byte word per thread, grid-stride)
+// ===========================================================================
+__global__ void k_synth_experts(uint8_t *arena_l, uint64_t seed, int layer) {
+    const uint64_t wpe = QE_EXPERT_BYTES / 8, total = wpe * QE_N_EXPERT;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (uint64_t)gridDim.x * blockDim.x) {
+        const int e = (int)(i / wpe);
+        ((uint64_t *)arena_l)[i] = qe_synth_expert_word(seed, layer, e, i % wpe);
+    }
+}
+__global__ void k_synth_router(float *router_l, uint64_t seed, int layer) {
+    const int n = QE_ROUTER_ROWS * QE_D;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
+        router_l[i] = qe_synth_router(seed, layer, i / QE_D, i % QE_D);
+}
+__global__ void k_synth_q8(uint8_t *dst, uint64_t seed, int layer, uint32_t tensor, int cols, uint64_t nwords) {
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < nwords; i += (uint64_t)gridDim.x * blockDim.x)
+        ((uint64_t *)dst)[i] = qe_synth_q8_word(seed, layer, tensor, cols, i);
+}
+__global__ void k_synth_x(float *out, uint64_t seed, int inst, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        out[i] = qe_synth_x(seed, inst, (uint64_t)i);
+}
+__global__ void k_fill_f32(float *p, float v, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) p[i] = v;
+}
+
+// ===========================================================================
+// host launchers
+// ===========================================================================
+// Event bracket of one launch when per-kernel timing is on.
+struct ProfScope {
+    QeProf *p;
+    hipStream_t st;
+    int slot = -1;
+    ProfScope(QeProf *p_, int kid, hipStream_t s) : p(p_), st(s) {
+        if (!p || !p->on) return;
+        if (p->used >= p->cap) { p->dropped++; return; }
+        slot = p->used++;
+        p->kid[slot] = kid;
+        (void)hipEventRecord(p->ev[2 * slot], st);
+    }
+    ~ProfScope() {
+        if (slot >= 0) (void)hipEventRecord(p->ev[2 * slot + 1], st);
+    }
+};
+#define QE_PROF(kid) ProfScope prof_scope_##kid(S.prof, kid, st)
+
+hipError_t qe_launch_layer(const QeLayerPtrs &L, const QeScratch &S, const float *xin, bool norm, const float *x2,
+                           float *out, int T, hipStream_t st) {
+    const float *pn = norm ? L.post_norm : nullptr;
+    const int np = T * QE_K_USED;
+    QeExpertArgs ea{L.arena, S.xq, S.xs, S.pairs, S.items, S.n_items, S.h};
+    QeDownArgs da{L.arena, L.sh_dn, T, S.h, S.hq, S.hs, S.shgu, S.pairs, S.items, S.n_items,
+                  S.wts, S.shg, x2, S.yp, S.sd, out};
+    if (T <= QE_SMALL_T) {
+        QeRouteArgs ra{xin, T, pn, L.router, L.bias, L.sh_gu, S.xn, S.xq, S.xs, S.logits, S.shgu,
+                       S.ids, S.wts, S.shg, S.off, S.pairs, S.items, S.n_items, S.counter};
+        {
+            QE_PROF(QP_ROUTE_SMALL);
+            k_route_small<<<(QE_ROUTER_ROWS + QE_SH_GU_ROWS + 3) / 4, 256, 0, st>>>(ra);
+        }
+        {
+            QE_PROF(QP_GU);
+            k_gu<QE_SMALL_T><<<dim3(np < QE_N_EXPERT ? np : QE_N_EXPERT, QE_FF_EXP / 16), 256, 0, st>>>(ea);
+        }
+        {
+            QE_PROF(QP_DOWN_SMALL);
+            k_down_small<<<QE_D / 8, 128, 0, st>>>(da);
+        }
+        return hipGetLastError();
+    }
+    const int mt = (T + 63) / 64;
+    {
+        QE_PROF(QP_NORMQ);
+        k_normq<<<(T + 3) / 4, 256, 0, st>>>(xin, T, pn, S.xn, S.xq, S.xs);
+    }
+    {
+        QE_PROF(QP_ROUTER);
+        k_gemm_canon<GEMM_ROUTER><<<dim3((QE_ROUTER_ROWS + 63) / 64, mt), 256, 0, st>>>(
+            QeGemmArgs{S.xn, T, L.router, nullptr, L.bias, S.logits});
+    }
+    {
+        QE_PROF(QP_SHGU);
+        k_gemm_canon<GEMM_SHGU><<<dim3(QE_SH_GU_ROWS / 64, mt), 256, 0, st>>>(
+            QeGemmArgs{S.xn, T, nullptr, L.sh_gu, nullptr, S.shgu});
+    }
+    {
+        QE_PROF(QP_TOPK);
+        k_topk<<<(T + 3) / 4, 256, 0, st>>>(S.logits, T, S.ids, S.wts, S.shg);
+    }
+    {
+        QE_PROF(QP_DISPATCH);
+        (void)qe_launch_dispatch(S, T, st);
+    }
+    const int max_items = np / QE_LARGE_TC + QE_N_EXPERT;
+    {
+        QE_PROF(QP_GU);
+        k_gu<QE_LARGE_TC><<<dim3(max_items, QE_FF_EXP / 16), 256, 0, st>>>(ea);
+    }
+    {
+        QE_PROF(QP_HQUANT);
+        k_hquant<<<(np * (QE_FF_EXP / 32) + 255) / 256, 256, 0, st>>>(S.h, np * (QE_FF_EXP / 32), S.hq, S.hs);
+    }
+    {
+        QE_PROF(QP_DOWN_LARGE);
+        k_down_large<QE_LARGE_TC><<<dim3(max_items, QE_D / 64), 256, 0, st>>>(da);
+    }
+    {
+        QE_PROF(QP_SHDN);
+        k_gemm_canon<GEMM_SHDN><<<dim3(QE_D / 64, mt), 256, 0, st>>>(
+            QeGemmArgs{S.shgu, T, nullptr, L.sh_dn, nullptr, S.sd});
+    }
+    {
+        QE_PROF(QP_COMBINE);
+        k_combine<<<(unsigned)(((size_t)T * QE_D + 255) / 256), 256, 0, st>>>(da);
+    }
+    return hipGetLastError();
+}
+
+hipError_t qe_launch_dispatch(const QeScratch &S, int T, hipStream_t st) {
+    const int np = T * QE_K_USED, nch = (np + 1023) / 1024;
+    k_disp_hist<<<nch, 1024, 0, st>>>(S.ids, np, S.chunk_hist);
+    k_disp_scatter<<<nch, 1024, 0, st>>>(S.ids, np, S.chunk_hist, nch, QE_LARGE_TC, S.off, S.pairs, S.items,
+                                          S.n_items);
+    return hipGetLastError();
+}
+
+hipError_t qe_launch_synth_layer(uint8_t *arena_l, float *router_l, uint8_t *sh_gu_l, uint8_t *sh_dn_l,
+                                 float *post_norm_l, uint64_t seed, int layer, hipStream_t st) {
+    k_synth_experts<<<16384, 256, 0, st>>>(arena_l, seed, layer);
+    k_synth_router<<<1024, 256, 0, st>>>(router_l, seed, layer);
+    k_synth_q8<<<1024, 256, 0, st>>>(sh_gu_l, seed, layer, QE_T_SH_GU, QE_D, QE_SH_GU_BYTES / 8);
+    k_synth_q8<<<1024, 256, 0, st>>>(sh_dn_l, seed, layer, QE_T_SH_DN, QE_FF_SH, QE_SH_DN_BYTES / 8);
+    k_fill_f32<<<8, 256, 0, st>>>(post_norm_l, 1.0f, QE_D);
+    return hipGetLastError();
+}
+
+hipError_t qe_launch_synth_x(float *out, uint64_t seed, int inst, int64_t n, hipStream_t st) {
+    const int64_t blocks = (n + 255) / 256;
+    k_synth_x<<<(unsigned)(blocks < 4096 ? (blocks > 0 ? blocks : 1) : 4096), 256, 0, st>>>(out, seed, inst, n);
+    return hipGetLastError();
+}

@@ -1,0 +1,35 @@
+"""The C ABI library loads and exports every declared symbol (no GPU calls)."""
+import ctypes
+
+import pytest
+
+import qe_moe
+
+
+def test_library_exports_every_header_symbol():
+    lib = qe_moe.load()
+    names = qe_moe.header_symbols()
+    assert "qe_moe_forward" in names and "qe_moe_forward_normed" in names
+    for n in names:
+        assert hasattr(lib, n), n
+
+
+def test_expert_bytes_and_argument_errors():
+    lib = qe_moe.load()
+    assert lib.qe_moe_expert_bytes() == 1769472
+    h = ctypes.c_void_p()
+    assert lib.qe_moe_create(0, 0, 8, ctypes.byref(h)) == qe_moe.QE_ERR_ARG
+    assert b"bad argument" in lib.qe_moe_last_error()
+    assert lib.qe_moe_create(0, 1, 0, ctypes.byref(h)) == qe_moe.QE_ERR_ARG
+    assert lib.qe_moe_forward(None, 0, None, None, 1, None) == qe_moe.QE_ERR_ARG
+    assert lib.qe_moe_destroy(None) == 0
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    saved = qe_moe._lib
+    qe_moe._lib = None
+    try:
+        with pytest.raises(qe_moe.LibraryMissing):
+            qe_moe.load(str(tmp_path / "nope.so"))
+    finally:
+        qe_moe._lib = saved

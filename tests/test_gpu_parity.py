@@ -1,0 +1,222 @@
+"""GPU parity of the HIP MoE block against the CPU oracle (needs an MI355X).
+
+Bar (north star): routing ids, the dispatch permutation and offsets bit-exact;
+router logits bit-exact (canonical order shared with the oracle); layer
+outputs within 1e-3 relative L2, and the shared-expert term separately within
+1e-3 (it is ~1e-5 of the output norm, so the total does not constrain it).
+Weights are within 2e-6 (the GPU and the oracle use their own expf).
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+import qe_moe
+
+pytestmark = pytest.mark.gpu
+SEED = 0xC0FFEE
+TOL = 1e-3
+
+
+def rel_l2(a, b):
+    return float(np.linalg.norm(a.astype(np.float64) - b) / max(np.linalg.norm(b.astype(np.float64)), 1e-30))
+
+
+def say(msg):
+    print(msg, flush=True)
+
+
+@pytest.fixture(scope="module")
+def ctx(torch_cuda):
+    m = qe_moe.MoE(n_layers=2, t_max=8192)
+    yield m
+    m.close()
+
+
+_layers = {}
+
+
+def host_layer(layer, bias_s):
+    key = (layer, bias_s)
+    if key not in _layers:
+        bias = None if bias_s is None else O.gen_zipf_bias(SEED, layer, bias_s)
+        _layers[key] = O.SynthLayer(SEED, layer, bias=bias)
+    return _layers[key]
+
+
+def run_gpu(torch, ctx, layer, bias_s, x_host, norm=False):
+    L = host_layer(layer, bias_s)
+    ctx.synth_layer(layer, SEED, L.bias)
+    x = torch.from_numpy(x_host).cuda()
+    y = torch.empty_like(x)
+    T = x_host.shape[0]
+    if norm:
+        ctx.forward(layer, x, y, T)
+    else:
+        ctx.forward_normed(layer, x, y, T)
+    torch.cuda.synchronize()
+    r = ctx.routing(T)
+    r["logits"] = ctx.logits(T)
+    r["out"] = y.cpu().numpy()
+    return L, r
+
+
+def check_layer(L, g, x, norm=False, sample=None):
+    T = x.shape[0]
+    ref_in = x if sample is None else x[sample]
+    o = O.moe_layer(L, ref_in, norm=norm, residual=norm)
+    gi = slice(None) if sample is None else sample
+    assert np.array_equal(g["logits"][gi].view(np.uint32), o["logits"].view(np.uint32)), "router logits differ"
+    assert np.array_equal(g["ids"][gi], o["ids"]), "routing ids differ"
+    assert np.abs(g["wts"][gi] - o["wts"]).max() <= 2e-6
+    assert np.abs(g["shg"][gi] - o["shg"]).max() <= 2e-6
+    if sample is None:
+        assert np.array_equal(g["off"], o["off"]) and np.array_equal(g["pairs"], o["pairs"]), "dispatch differs"
+    e_out = rel_l2(g["out"][gi], o["out"])
+    e_sd = rel_l2(g["sd"][gi], o["sd"])
+    say(f"  T={T} out rel-L2 {e_out:.2e}  shared rel-L2 {e_sd:.2e}")
+    assert e_out <= TOL and e_sd <= TOL
+    return o
+
+
+def test_synthetic_bytes_match_host_generator(ctx, torch_cuda):
+    torch = torch_cuda
+    say("synth bytes: layer 0")
+    ctx.synth_layer(0, SEED, None)
+    torch.cuda.synchronize()
+    base = ctx.arena_ptr(0)
+    import ctypes
+    hip = ctypes.CDLL("libamdhip64.so")
+    for e in (0, 1, 137, 255):
+        buf = np.empty(O.EXPERT_BYTES, np.uint8)
+        assert hip.hipMemcpy(ctypes.c_void_p(buf.ctypes.data), ctypes.c_void_p(base + e * O.EXPERT_BYTES),
+                             ctypes.c_size_t(O.EXPERT_BYTES), 2) == 0
+        assert np.array_equal(buf, O.gen_expert(SEED, 0, e)), e
+    x = torch.empty(3 * 2048, device="cuda")
+    qe_moe.synth_x(SEED, 5, x, x.numel())
+    assert np.array_equal(x.cpu().numpy().reshape(3, 2048), O.gen_x(SEED, 5, 3))
+
+
+@pytest.mark.parametrize("T", [1, 2, 5])
+def test_decode_small_T_no_bias(ctx, torch_cuda, T):
+    say(f"decode T={T} no bias")
+    x = O.gen_x(SEED, 100 + T, T)
+    L, g = run_gpu(torch_cuda, ctx, 0, None, x)
+    check_layer(L, g, x)
+
+
+def test_cfg0_decode_B1(ctx, torch_cuda):
+    say("config 0: B=1")
+    x = O.gen_x(SEED, 0, 1)
+    L, g = run_gpu(torch_cuda, ctx, 0, None, x)
+    check_layer(L, g, x)
+
+
+def test_cfg1_decode_B8_zipf(ctx, torch_cuda):
+    say("config 1: B=8, Zipf s=1.0 bias")
+    x = O.gen_x(SEED, 1, 8)
+    L, g = run_gpu(torch_cuda, ctx, 1, 1.0, x)
+    check_layer(L, g, x)
+
+
+@pytest.mark.parametrize("T", [1, 8, 9, 16])
+def test_forward_with_norm_and_residual(ctx, torch_cuda, T):
+    say(f"forward (norm + residual) T={T}")
+    x = O.gen_x(SEED, 200 + T, T)
+    L, g = run_gpu(torch_cuda, ctx, 1, 1.0, x, norm=True)
+    check_layer(L, g, x, norm=True)
+
+
+def test_cfg3_prefill_512(ctx, torch_cuda):
+    say("config 3: prefill 512, Zipf s=1.0")
+    x = O.gen_x(SEED, 3, 512)
+    L, g = run_gpu(torch_cuda, ctx, 0, 1.0, x)
+    o = check_layer(L, g, x)
+    cnt = np.diff(o["off"])
+    say(f"  distinct experts {np.count_nonzero(cnt)}, max tokens/expert {cnt.max()}")
+
+
+def test_cfg4_prefill_8192_skewed(ctx, torch_cuda):
+    say("config 4: prefill 8192, Zipf s=1.3 (routing on all tokens, outputs on a sample)")
+    x = O.gen_x(SEED, 4, 8192)
+    L, g = run_gpu(torch_cuda, ctx, 1, 1.3, x)
+    lg = O.router(x, L.router, L.bias)
+    assert np.array_equal(g["logits"].view(np.uint32), lg.view(np.uint32))
+    ids, _, _ = O.topk(lg)
+    assert np.array_equal(g["ids"], ids)
+    off, pairs = O.dispatch(ids)
+    assert np.array_equal(g["off"], off) and np.array_equal(g["pairs"], pairs)
+    sample = np.sort(np.random.default_rng(4).choice(8192, 96, replace=False))
+    check_layer(L, g, x, sample=sample)
+    cnt = np.diff(off)
+    say(f"  distinct {np.count_nonzero(cnt)}, max/expert {cnt.max()}, <4 tokens {int(((cnt > 0) & (cnt < 4)).sum())}")
+
+
+def test_dispatch_on_reference_routing_records(ctx, torch_cuda):
+    import os
+    torch = torch_cuda
+    fx = np.load(os.path.join(os.path.dirname(__file__), "golden", "routing_records.npz"))
+    for name in sorted({k.rsplit("_", 1)[0] for k in fx.files}):
+        say(f"dispatch fixture {name}")
+        ids = torch.from_numpy(fx[name + "_ids"].astype(np.int32)).cuda()
+        T = ids.shape[0]
+        ctx.dispatch(ids, T)
+        r = ctx.routing(T)
+        assert np.array_equal(r["off"], fx[name + "_off"]) and np.array_equal(r["pairs"], fx[name + "_pairs"])
+
+
+def test_dispatch_extremes(ctx, torch_cuda):
+    torch = torch_cuda
+    rng = np.random.default_rng(9)
+    # all tokens on the same 8 experts (maximal skew), and the maximum T
+    for T, ids in ((8192, np.tile(np.arange(8, dtype=np.int32)[::-1], (8192, 1))),
+                   (8192, np.stack([rng.choice(256, 8, replace=False) for _ in range(8192)]).astype(np.int32)),
+                   (3, np.array([[255, 0, 1, 2, 3, 4, 5, 6]] * 3, np.int32))):
+        say(f"dispatch extreme T={T}")
+        ctx.dispatch(torch.from_numpy(ids).cuda(), T)
+        r = ctx.routing(T)
+        off, pairs = O.dispatch(ids)
+        assert np.array_equal(r["off"], off) and np.array_equal(r["pairs"], pairs)
+
+
+def test_stack_teacher_forced(torch_cuda):
+    """Config 2 structure on 3 layers: each GPU layer consumes the oracle's input h_l."""
+    torch = torch_cuda
+    n = 3
+    m = qe_moe.MoE(n_layers=n, t_max=8)
+    try:
+        h = O.gen_x(SEED, 77, 1)
+        for l in range(n):
+            m.synth_layer(l, SEED + 1000, None)
+        x_in = torch.from_numpy(h).cuda()
+        x_out = torch.empty_like(x_in)
+        m.forward_stack(0, n, x_in, x_out, 1)
+        torch.cuda.synchronize()
+        stack_gpu = x_out.cpu().numpy()
+        for l in range(n):
+            say(f"stack layer {l}")
+            L = O.SynthLayer(SEED + 1000, l)
+            xi = torch.from_numpy(h).cuda()
+            yo = torch.empty_like(xi)
+            m.forward(l, xi, yo, 1)
+            torch.cuda.synchronize()
+            g = m.routing(1)
+            g["logits"] = m.logits(1)
+            g["out"] = yo.cpu().numpy()
+            o = check_layer(L, g, h, norm=True)
+            h = o["out"]
+        say(f"  end-to-end stack drift rel-L2 {rel_l2(stack_gpu, h):.2e}")
+        assert rel_l2(stack_gpu, h) <= TOL
+    finally:
+        m.close()
+
+
+def test_errors_are_reported(ctx, torch_cuda):
+    torch = torch_cuda
+    x = torch.zeros(1, 2048, device="cuda")
+    with pytest.raises(qe_moe.QeError) as e:
+        ctx.forward_normed(0, x, x, 1)
+    assert e.value.code == qe_moe.QE_ERR_ARG
+    with pytest.raises(qe_moe.QeError):
+        ctx.forward_normed(0, x, torch.empty_like(x), 8193)
+    with pytest.raises(qe_moe.QeError):
+        ctx.forward_normed(5, x, torch.empty_like(x), 1)

@@ -1,0 +1,298 @@
+"""Pins of the CPU oracle (CPU only).
+
+The reference holds no golden vectors for the MoE path (its only numeric
+check, `qe check`, needs real weights and llama.cpp).  Each oracle function is
+pinned here by closed forms, special cases, brute force or an independent
+restatement, chosen so a plausible slip (dropped term, wrong sign/index,
+transposed operand, wrong rounding or tie rule) fails a check.
+"""
+import math
+import os
+import re
+
+import numpy as np
+import pytest
+
+import oracle as O
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+KV = np.array([-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113], np.int64)
+SEED = 0x5EED
+
+
+def _header_consts():
+    txt = open(os.path.join(REPO, "qe-qwen36-b50_amd", "csrc", "qe_format.h")).read()
+    return {m[0]: int(m[1], 16) for m in re.findall(r"#define (QE_NL4_W\d) (0x[0-9A-Fa-f]+)u", txt)}
+
+
+def test_codebook_words_match_reference_constants():
+    w = _header_consts()
+    packed = np.array(KV, np.int8).view(np.uint8).tobytes()
+    assert [w["QE_NL4_W%d" % i] for i in range(4)] == list(np.frombuffer(packed, "<u4"))
+    # engine/qe.cpp:78-79 packs the same table as two 64-bit constants
+    assert (w["QE_NL4_W1"] << 32) | w["QE_NL4_W0"] == 0xF6EADDCFBFAD9881
+    assert (w["QE_NL4_W3"] << 32) | w["QE_NL4_W2"] == 0x7159453526190D01
+
+
+def test_row_and_blob_sizes():
+    # engine/pack.h:28-42 closed forms
+    assert 2048 // 2 + 2048 // 32 * 2 == 1152
+    assert 512 // 2 + 512 // 32 * 2 == 288
+    assert 2 * 512 * 1152 + 2048 * 288 == O.EXPERT_BYTES == 1769472
+    assert O.SH_GU_BYTES == 1024 * (2048 + 128) and O.SH_DN_BYTES == 2048 * (512 + 32)
+    assert len(O.gen_expert(SEED, 0, 0)) == 1769472
+
+
+def test_f16_conversion_matches_ieee_rne():
+    lib = O.load()
+    rng = np.random.default_rng(1)
+    vals = np.concatenate([
+        rng.standard_normal(20000).astype(np.float32) * np.float32(0.02),
+        (rng.random(20000) * 2.0 ** rng.integers(-30, 17, 20000)).astype(np.float32),
+        np.array([0.0, -0.0, 65504, 65519.99, 65520, 1e-8, 2.0 ** -24, 2.0 ** -25, 3 * 2.0 ** -26, 0.0005], np.float32),
+    ])
+    got = np.array([lib.orc_f32_to_f16(float(v)) for v in vals], np.uint16)
+    want = vals.astype(np.float16).view(np.uint16)
+    assert np.array_equal(got, want)
+    allh = np.arange(65536, dtype=np.uint16)
+    fin = np.isfinite(allh.view(np.float16))
+    back = np.array([lib.orc_f16_to_f32(int(h)) for h in allh[fin]], np.float32)
+    assert np.array_equal(back.view(np.uint32), allh[fin].view(np.float16).astype(np.float32).view(np.uint32))
+
+
+def test_log_and_cos_against_libm():
+    lib = O.load()
+    rng = np.random.default_rng(2)
+    for u in list(rng.random(2000) + 1e-12) + [1.0, 2.0 ** -32, 0.5, math.sqrt(0.5)]:
+        assert abs(lib.orc_log_unit(u) - math.log(u)) <= 4e-16 * max(1.0, abs(math.log(u)))
+    for t in list(rng.random(2000)) + [0.0, 0.25, 0.5, 0.75, 0.999999]:
+        assert abs(lib.orc_cos_turns(t) - math.cos(2 * math.pi * t)) <= 2e-15
+
+
+def test_normal_moments():
+    x = O.gen_x(SEED, 7, 64).reshape(-1).astype(np.float64)  # 131072 samples
+    assert abs(x.mean()) < 0.01 and abs(x.std() - 1.0) < 0.01
+    assert abs(((x - x.mean()) ** 3).mean()) < 0.03 and abs((x ** 4).mean() - 3.0) < 0.06
+
+
+def _quant_ref(x):
+    """numpy restatement of quant_x (float32 arithmetic, round half to even)."""
+    x = x.astype(np.float32).reshape(-1, 32)
+    amax = np.abs(x).max(axis=1)
+    d = (amax / np.float32(127)).astype(np.float32)
+    with np.errstate(divide="ignore"):
+        idv = np.where(d > 0, np.float32(1) / d, np.float32(0)).astype(np.float32)
+    q = np.clip(np.rint(x * idv[:, None]), -128, 127).astype(np.int8)
+    return q.reshape(-1), d
+
+
+def test_quant_x_special_cases():
+    z = np.zeros(32, np.float32)
+    q, s = O.quant_x(z)
+    assert s[0] == 0 and not q.any()
+    x = np.zeros(32, np.float32)
+    x[5] = -3.0
+    q, s = O.quant_x(x)
+    assert q[5] == -127 and np.count_nonzero(q) == 1 and s[0] == np.float32(3.0) / np.float32(127)
+    # amax 127 -> d = 1 exactly: halves round to even
+    x = np.array([127, 2.5, 3.5, -2.5, -3.5, 0.5, -0.5, 1.5] + [0] * 24, np.float32)
+    q, s = O.quant_x(x)
+    assert s[0] == 1.0 and list(q[:8]) == [127, 2, 4, -2, -4, 0, 0, 2]
+    x = -x
+    q, _ = O.quant_x(x)
+    assert q[0] == -127
+
+
+def test_quant_x_scalar_avx2_and_numpy_agree():
+    rng = np.random.default_rng(3)
+    for scale in (1.0, 1e-3, 1e4):
+        x = (rng.standard_normal(2048) * scale).astype(np.float32)
+        q1, s1 = O.quant_x(x)
+        q2, s2 = O.quant_x(x, avx2=True)
+        q3, s3 = _quant_ref(x)
+        assert np.array_equal(q1, q2) and np.array_equal(q1, q3)
+        assert np.array_equal(s1.view(np.uint32), s2.view(np.uint32)) and np.array_equal(s1, s3)
+
+
+def _decode_nl4_row(row, cols):
+    codes = row[: cols // 2].reshape(-1, 16)
+    lo, hi = codes & 15, codes >> 4
+    idx = np.concatenate([lo, hi], axis=1).reshape(-1)  # element j<16 low nibble of byte j, j+16 high
+    scales = row[cols // 2: cols // 2 + cols // 32 * 2].view(np.float16).astype(np.float64)
+    return KV[idx], scales
+
+
+def test_dot_nl4_brute_force_and_forms_agree():
+    rng = np.random.default_rng(4)
+    blob = O.gen_expert(SEED, 0, 3)
+    for cols, off, rb in ((2048, 0, 1152), (2048, 700 * 1152, 1152), (512, 1179648 + 99 * 288, 288)):
+        row = blob[off: off + rb]
+        x = rng.standard_normal(cols).astype(np.float32)
+        xq, xs = O.quant_x(x)
+        a = O.dot_nl4(row, cols, xq, xs)
+        b = O.dot_nl4(row, cols, xq, xs, avx2=True)
+        assert np.float32(a).view(np.uint32) == np.float32(b).view(np.uint32)
+        w, sc = _decode_nl4_row(row, cols)
+        p = (w.reshape(-1, 32) * xq.astype(np.int64).reshape(-1, 32)).sum(axis=1)  # exact per-block int dots
+        exact = float((sc * xs.astype(np.float64) * p).sum())
+        assert abs(a - exact) <= 2e-6 * np.abs(sc * xs * p).sum()
+    # a transposed nibble order (element j+16 taken from the low nibble) must not pass
+    wrong = KV[np.concatenate([row[:256].reshape(-1, 16) >> 4, row[:256].reshape(-1, 16) & 15], 1).reshape(-1)]
+    assert not np.array_equal(wrong, _decode_nl4_row(row, 512)[0])
+
+
+def test_canon_dot_and_rmsnorm():
+    rng = np.random.default_rng(5)
+    a = rng.standard_normal(2048).astype(np.float32)
+    b = rng.standard_normal(2048).astype(np.float32)
+    exact = float(np.dot(a.astype(np.float64), b.astype(np.float64)))
+    assert abs(O.canon_dot(a, b) - exact) <= 1e-5 * float(np.abs(a.astype(np.float64) * b).sum())
+    # exactly representable case: every partial is an integer
+    ai = rng.integers(-8, 8, 2048).astype(np.float32)
+    assert O.canon_dot(ai, ai) == float((ai.astype(np.int64) ** 2).sum())
+    x = rng.standard_normal((3, 2048)).astype(np.float32)
+    w = rng.random(2048).astype(np.float32) + 0.5
+    xn = O.rmsnorm(x, w)
+    ref = x / np.sqrt((x.astype(np.float64) ** 2).mean(axis=1, keepdims=True) + 1e-6) * w
+    assert np.abs(xn - ref).max() <= 2e-6 * np.abs(ref).max()
+    c = np.full((1, 2048), 3.0, np.float32)
+    assert np.allclose(O.rmsnorm(c, np.ones(2048, np.float32)), 3.0 / math.sqrt(9.0 + 1e-6), rtol=1e-7)
+
+
+def _topk_ref(lg):
+    """Closed form of engine/qe.cpp:1454-1483: order by (-value, e % 16, e // 16)."""
+    e = np.arange(256)
+    order = sorted(e, key=lambda i: (-float(lg[i]), i % 16, i // 16))
+    return np.array(order[:8])
+
+
+def test_topk_all_equal_and_ties():
+    lg = np.zeros((1, 257), np.float32)
+    ids, wts, shg = O.topk(lg)
+    assert list(ids[0]) == [0, 16, 32, 48, 64, 80, 96, 112]
+    assert np.allclose(wts, 0.125) and shg[0] == 0.5
+    rng = np.random.default_rng(6)
+    for trial in range(200):
+        lg = rng.integers(-3, 3, size=257).astype(np.float32)  # many ties
+        ids, _, _ = O.topk(lg[None])
+        assert list(ids[0]) == list(_topk_ref(lg)), trial
+    # -0.0 and +0.0 tie
+    lg = np.full(257, -5.0, np.float32)
+    lg[33], lg[2] = -0.0, 0.0
+    ids, _, _ = O.topk(lg[None])
+    assert list(ids[0][:2]) == [33, 2]  # 33 % 16 = 1 < 2 % 16 = 2
+
+
+def test_topk_distinct_and_weights():
+    rng = np.random.default_rng(7)
+    lg = rng.standard_normal((64, 257)).astype(np.float32)
+    ids, wts, shg = O.topk(lg)
+    for t in range(64):
+        want = np.argsort(-lg[t, :256], kind="stable")[:8]
+        assert np.array_equal(ids[t], want)
+        sel = lg[t, ids[t]].astype(np.float64)
+        p = np.exp(sel - sel[0])
+        assert np.allclose(wts[t], p / p.sum(), rtol=2e-6, atol=0)
+        assert abs(shg[t] - 1 / (1 + math.exp(-float(lg[t, 256])))) < 1e-6
+
+
+def test_dispatch_fixture_and_random():
+    fx = np.load(os.path.join(REPO, "tests", "golden", "routing_records.npz"))
+    names = sorted({k.rsplit("_", 1)[0] for k in fx.files})
+    assert names
+    for n in names:
+        off, pairs = O.dispatch(fx[n + "_ids"].astype(np.int32))
+        assert np.array_equal(off, fx[n + "_off"]) and np.array_equal(pairs, fx[n + "_pairs"])
+    rng = np.random.default_rng(8)
+    for T in (1, 7, 300):
+        ids = np.stack([rng.choice(256, 8, replace=False) for _ in range(T)]).astype(np.int32)
+        off, pairs = O.dispatch(ids)
+        flat = ids.reshape(-1)
+        assert np.array_equal(pairs, np.argsort(flat, kind="stable"))
+        assert np.array_equal(np.diff(off), np.bincount(flat, minlength=256))
+
+
+def _f64_layer(L, x, ids, wts, shg):
+    """Independent float64 restatement of one layer from the raw bytes."""
+    T = x.shape[0]
+    out = np.zeros((T, 2048))
+    sgu = L.sh_gu.reshape(1024, 2176)
+    Wsh = sgu[:, :2048].view(np.int8).astype(np.float64) * np.repeat(sgu[:, 2048:].view(np.float16).astype(np.float64), 32, 1)
+    sdn = L.sh_dn.reshape(2048, 544)
+    Dsh = sdn[:, :512].view(np.int8).astype(np.float64) * np.repeat(sdn[:, 512:].view(np.float16).astype(np.float64), 32, 1)
+    exps = L.experts(ids)
+    for t in range(T):
+        xq, xs = _quant_ref(x[t])
+        xd = xq.astype(np.float64) * np.repeat(xs.astype(np.float64), 32)
+        g, u = Wsh[:512] @ x[t].astype(np.float64), Wsh[512:] @ x[t].astype(np.float64)
+        hsh = g / (1 + np.exp(-g)) * u
+        acc = shg[t] * (Dsh @ hsh)
+        for k in range(8):
+            blob = exps[int(ids[t, k])]
+            rows = blob[:1179648].reshape(1024, 1152)
+            W = np.stack([np.repeat(_decode_nl4_row(r, 2048)[1], 32) * _decode_nl4_row(r, 2048)[0] for r in rows])
+            gu = W @ xd
+            with np.errstate(over="ignore"):
+                h = gu[:512] / (1 + np.exp(-gu[:512])) * gu[512:]
+            hq, hs = _quant_ref(h.astype(np.float32))
+            hd = hq.astype(np.float64) * np.repeat(hs.astype(np.float64), 32)
+            drows = blob[1179648:].reshape(2048, 288)
+            Dm = np.stack([np.repeat(_decode_nl4_row(r, 512)[1], 32) * _decode_nl4_row(r, 512)[0] for r in drows])
+            acc = acc + wts[t, k] * (Dm @ hd)
+        out[t] = acc
+    return out
+
+
+def test_full_layer_against_float64_restatement():
+    L = O.SynthLayer(SEED, 0)
+    x = O.gen_x(SEED, 1, 1)
+    r = O.moe_layer(L, x)
+    ref = _f64_layer(L, x, r["ids"], r["wts"].astype(np.float64), r["shg"].astype(np.float64))
+    rel = np.linalg.norm(r["out"] - ref) / np.linalg.norm(ref)
+    assert rel < 1e-4, rel
+    # the shared-expert term on its own (it is ~1e-5 of the output norm)
+    sgu = L.sh_gu.reshape(1024, 2176)
+    Wsh = sgu[:, :2048].view(np.int8).astype(np.float64) * np.repeat(sgu[:, 2048:].view(np.float16).astype(np.float64), 32, 1)
+    sdn = L.sh_dn.reshape(2048, 544)
+    Dsh = sdn[:, :512].view(np.int8).astype(np.float64) * np.repeat(sdn[:, 512:].view(np.float16).astype(np.float64), 32, 1)
+    g, u = Wsh[:512] @ x[0].astype(np.float64), Wsh[512:] @ x[0].astype(np.float64)
+    sd = Dsh @ (g / (1 + np.exp(-g)) * u)
+    assert np.linalg.norm(r["sd"][0] - sd) / np.linalg.norm(sd) < 1e-6
+
+
+def test_scalar_and_avx2_layers_agree_bitwise():
+    L = O.SynthLayer(SEED, 1, bias=O.gen_zipf_bias(SEED, 1, 1.0))
+    x = O.gen_x(SEED, 2, 3)
+    ids, wts, _ = O.topk(O.router(x, L.router, L.bias))
+    ya = O.routed(x, ids, wts, L.experts(ids), avx2=True)
+    ys = O.routed(x, ids, wts, L.experts(ids), avx2=False)
+    assert np.array_equal(ya.view(np.uint32), ys.view(np.uint32))
+
+
+def test_baseline_layer_matches_oracle():
+    import ctypes
+    L = O.SynthLayer(SEED, 2, bias=O.gen_zipf_bias(SEED, 2, 1.0))
+    x = O.gen_x(SEED, 3, 4)
+    r = O.moe_layer(L, x)
+    exps = L.experts(r["ids"])
+    ptrs = (ctypes.c_void_p * 256)()
+    for e, b in exps.items():
+        ptrs[e] = b.ctypes.data
+    _, out = O.baseline_layer(x, None, L, ptrs, 4, 4)
+    assert np.linalg.norm(out - r["out"]) / np.linalg.norm(r["out"]) < 1e-5
+    # with norm + residual (config 2's layer)
+    pn = np.ones(2048, np.float32)
+    r2 = O.moe_layer(L, x, norm=True, residual=True)
+    exps = L.experts(r2["ids"])
+    for e, b in exps.items():
+        ptrs[e] = b.ctypes.data
+    _, out2 = O.baseline_layer(x, pn, L, ptrs, 4, 4)
+    assert np.linalg.norm(out2 - r2["out"]) / np.linalg.norm(r2["out"]) < 1e-5
+
+
+def test_zipf_bias_is_a_permutation_of_log_ranks():
+    b = O.gen_zipf_bias(SEED, 0, 1.0)
+    ranks = np.sort(np.round(np.exp(-b.astype(np.float64))).astype(int))
+    assert np.array_equal(ranks, np.arange(1, 257))
+    b13 = O.gen_zipf_bias(SEED, 0, 1.3)
+    assert np.allclose(b13, 1.3 * b, rtol=1e-6)
