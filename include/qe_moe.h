@@ -111,7 +111,7 @@ int qe_moe_get_logits(qe_moe_ctx *ctx, int T, float *logits, void *stream);
  * events on its own stream.  qe_moe_profile_read sums the elapsed time and
  * launch count per kernel id (arrays of at least QE_MOE_NPROF entries), then
  * clears the record; qe_moe_profile_name names an id. */
-#define QE_MOE_NPROF 12
+#define QE_MOE_NPROF 11
 int qe_moe_profile(qe_moe_ctx *ctx, int enable);
 int qe_moe_profile_read(qe_moe_ctx *ctx, double *ms, int *launches, int n);
 const char *qe_moe_profile_name(int id);

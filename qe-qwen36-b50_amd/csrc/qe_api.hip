@@ -39,6 +39,10 @@ struct qe_moe_ctx {
     std::vector<uint8_t> has_bias, ready;
     QeScratch S{};
     QeProf prof;
+    uint8_t *bias_on = nullptr;  // device copy of has_bias
+    uint64_t *ex = nullptr;      // decode exchange words
+    unsigned *sync = nullptr;    // decode launch epoch + exit counter
+    unsigned *err = nullptr;     // decode barrier timeout flag
     float *pingpong[2] = {nullptr, nullptr};
     std::vector<void *> allocs;
 };
@@ -117,6 +121,11 @@ int qe_moe_create(int device, int n_layers, int t_max, qe_moe_ctx **out) {
     A(S.yp, NP * QE_D * 4);
     A(S.chunk_hist, nch * QE_N_EXPERT * 4);
     A(S.counter, 256);
+    A(c->bias_on, L);
+    A(c->ex, (size_t)(2 * QE_SMALL_T * QE_D + QE_SMALL_T * QE_ROUTER_ROWS + QE_SMALL_T * QE_SH_GU_ROWS +
+                      QE_SMALL_T * QE_K_USED * QE_FF_EXP) * 8);
+    A(c->sync, 8192);
+    A(c->err, 256);
     A(c->pingpong[0], T * QE_D * 4);
     A(c->pingpong[1], T * QE_D * 4);
 #undef A
@@ -128,6 +137,10 @@ int qe_moe_create(int device, int n_layers, int t_max, qe_moe_ctx **out) {
     S.t_max = t_max;
     S.prof = &c->prof;
     if (hipMemset(S.counter, 0, 256) != hipSuccess || hipMemset(c->bias, 0, L * QE_N_EXPERT * 4) != hipSuccess ||
+        hipMemset(c->bias_on, 0, L) != hipSuccess || hipMemset(c->sync, 0, 8192) != hipSuccess ||
+        hipMemset(c->err, 0, 256) != hipSuccess ||
+        hipMemset(c->ex, 0, (size_t)(2 * QE_SMALL_T * QE_D + QE_SMALL_T * QE_ROUTER_ROWS + QE_SMALL_T * QE_SH_GU_ROWS +
+                                     QE_SMALL_T * QE_K_USED * QE_FF_EXP) * 8) != hipSuccess ||
         hipDeviceSynchronize() != hipSuccess) {
         free_all(c);
         delete c;
@@ -171,6 +184,7 @@ int qe_moe_set_dense(qe_moe_ctx *c, int layer, const float *post_norm, const flo
     if (bias) {
         HIP_TRY(hipMemcpyAsync(c->bias + (size_t)layer * QE_N_EXPERT, bias, QE_N_EXPERT * 4, k, s));
         c->has_bias[layer] = 1;
+        HIP_TRY(hipMemcpyAsync(c->bias_on + layer, &c->has_bias[layer], 1, hipMemcpyHostToDevice, s));
     }
     if (sh_gu) HIP_TRY(hipMemcpyAsync((void *)L.sh_gu, sh_gu, QE_SH_GU_BYTES, k, s));
     if (sh_down) HIP_TRY(hipMemcpyAsync((void *)L.sh_dn, sh_down, QE_SH_DN_BYTES, k, s));
@@ -188,11 +202,31 @@ static int check_fwd(qe_moe_ctx *c, int layer, const void *in, const void *out, 
     return QE_OK;
 }
 
+// T <= QE_SMALL_T: every layer of the range in one persistent launch.
+static hipError_t run_decode(qe_moe_ctx *c, int first, int n, const float *in, float *out, int T, bool norm_res,
+                             hipStream_t st) {
+    QeDecodeArgs d{};
+    d.arena = c->arena; d.router = c->router; d.bias = c->bias; d.bias_on = c->bias_on;
+    d.sh_gu = c->sh_gu; d.sh_dn = c->sh_dn; d.post_norm = c->post_norm;
+    d.first_layer = first; d.n_layers = n; d.T = T; d.norm = norm_res; d.residual = norm_res;
+    d.x_in = in; d.x_out = out;
+    d.ex_x = c->ex;
+    d.ex_logits = d.ex_x + 2 * QE_SMALL_T * QE_D;
+    d.ex_shgu = d.ex_logits + QE_SMALL_T * QE_ROUTER_ROWS;
+    d.ex_h = d.ex_shgu + QE_SMALL_T * QE_SH_GU_ROWS;
+    d.logits = c->S.logits; d.ids = c->S.ids; d.wts = c->S.wts; d.shg = c->S.shg; d.off = c->S.off; d.pairs = c->S.pairs;
+    d.sd_out = c->S.sd; d.xn_out = c->S.xn;
+    d.sync = c->sync; d.err = c->err;
+    ProfScope ps(&c->prof, QP_DECODE, st);
+    return qe_launch_decode(d, st);
+}
+
 int qe_moe_forward(qe_moe_ctx *c, int layer, const float *x2, float *x, int T, void *stream) {
     int rc = check_fwd(c, layer, x2, x, T);
     if (rc) return rc;
     HIP_TRY(hipSetDevice(c->device));
-    HIP_TRY(qe_launch_layer(layer_ptrs(c, layer), c->S, x2, true, x2, x, T, (hipStream_t)stream));
+    if (T <= QE_SMALL_T) HIP_TRY(run_decode(c, layer, 1, x2, x, T, true, (hipStream_t)stream));
+    else HIP_TRY(qe_launch_layer(layer_ptrs(c, layer), c->S, x2, true, x2, x, T, (hipStream_t)stream));
     return QE_OK;
 }
 
@@ -200,7 +234,8 @@ int qe_moe_forward_normed(qe_moe_ctx *c, int layer, const float *xn, float *y, i
     int rc = check_fwd(c, layer, xn, y, T);
     if (rc) return rc;
     HIP_TRY(hipSetDevice(c->device));
-    HIP_TRY(qe_launch_layer(layer_ptrs(c, layer), c->S, xn, false, nullptr, y, T, (hipStream_t)stream));
+    if (T <= QE_SMALL_T) HIP_TRY(run_decode(c, layer, 1, xn, y, T, false, (hipStream_t)stream));
+    else HIP_TRY(qe_launch_layer(layer_ptrs(c, layer), c->S, xn, false, nullptr, y, T, (hipStream_t)stream));
     return QE_OK;
 }
 
@@ -208,6 +243,15 @@ int qe_moe_forward_stack(qe_moe_ctx *c, int first, int n, const float *x_in, flo
     if (!c || n <= 0 || first < 0 || first + n > c->n_layers)
         return fail(QE_ERR_ARG, "forward_stack: bad layer range");
     if (x_in == x_out) return fail(QE_ERR_ARG, "forward_stack: output may not alias the input");
+    if (T > 0 && T <= QE_SMALL_T) {
+        for (int i = 0; i < n; ++i) {
+            int rc = check_fwd(c, first + i, x_in, x_out, T);
+            if (rc) return rc;
+        }
+        HIP_TRY(hipSetDevice(c->device));
+        HIP_TRY(run_decode(c, first, n, x_in, x_out, T, true, (hipStream_t)stream));
+        return QE_OK;
+    }
     const float *cur = x_in;
     for (int i = 0; i < n; ++i) {
         float *dst = (i == n - 1) ? x_out : c->pingpong[i & 1];
@@ -230,7 +274,10 @@ int qe_moe_get_routing(qe_moe_ctx *c, int T, int32_t *ids, float *wts, float *sh
     if (off) HIP_TRY(hipMemcpyAsync(off, c->S.off, (QE_N_EXPERT + 1) * 4, hipMemcpyDeviceToHost, s));
     if (pairs) HIP_TRY(hipMemcpyAsync(pairs, c->S.pairs, np * 4, hipMemcpyDeviceToHost, s));
     if (shared_out) HIP_TRY(hipMemcpyAsync(shared_out, c->S.sd, (size_t)T * QE_D * 4, hipMemcpyDeviceToHost, s));
+    unsigned err = 0;
+    HIP_TRY(hipMemcpyAsync(&err, c->err, 4, hipMemcpyDeviceToHost, s));
     HIP_TRY(hipStreamSynchronize(s));
+    if (err) return fail(QE_ERR_STATE, "get_routing: a decode exchange poll timed out (results invalid)");
     return QE_OK;
 }
 
@@ -251,8 +298,8 @@ int qe_moe_get_logits(qe_moe_ctx *c, int T, float *logits, void *stream) {
 }
 
 static const char *const k_prof_names[QP_N] = {
-    "k_route_small", "k_gu", "k_down_small", "k_normq", "k_gemm_canon<router>", "k_gemm_canon<shared_gu>",
-    "k_topk", "k_disp_hist+k_disp_scatter", "k_hquant", "k_down_large", "k_gemm_canon<shared_down>", "k_combine"};
+    "k_decode", "k_normq", "k_gemm_canon<router>", "k_gemm_canon<shared_gu>", "k_topk", "k_disp_hist+k_disp_scatter",
+    "k_gu", "k_hquant", "k_down_large", "k_gemm_canon<shared_down>", "k_combine"};
 
 int qe_moe_profile(qe_moe_ctx *c, int enable) {
     if (!c) return fail(QE_ERR_ARG, "profile: bad argument");
@@ -306,11 +353,12 @@ int qe_moe_synth_layer(qe_moe_ctx *c, int layer, uint64_t seed, const float *bia
     if (bias) {
         HIP_TRY(hipMemcpyAsync(c->bias + (size_t)layer * QE_N_EXPERT, bias, QE_N_EXPERT * 4, hipMemcpyHostToDevice,
                                (hipStream_t)stream));
-        HIP_TRY(hipStreamSynchronize((hipStream_t)stream));
         c->has_bias[layer] = 1;
     } else {
         c->has_bias[layer] = 0;
     }
+    HIP_TRY(hipMemcpyAsync(c->bias_on + layer, &c->has_bias[layer], 1, hipMemcpyHostToDevice, (hipStream_t)stream));
+    HIP_TRY(hipStreamSynchronize((hipStream_t)stream));
     c->ready[layer] = 1;
     return QE_OK;
 }

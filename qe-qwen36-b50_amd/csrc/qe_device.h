@@ -95,3 +95,128 @@ QE_DEV float quant_scale_inv(float amax, float &d) {
 }
 
 QE_DEV float silu_mul(float g, float u) { return g / (1.f + expf(-g)) * u; }
+
+// ===========================================================================
+// top-8 of one token by one wave (engine/qe.cpp:1454-1483 semantics):
+// maximum logit first; ties go to the smaller (e % 16, e / 16), the order the
+// reference's 16-lane reduction produces.  Lane l holds e = l + 64 j.
+// ===========================================================================
+// v[j] = logit of expert lane + 64 j; lg_sh = logit 256 (shared-expert gate).
+QE_DEV void wave_topk_vals(float v[4], float lg_sh, int lane, int32_t *ids, float *wts, float *shg) {
+    float sel[QE_K_USED];
+    int id[QE_K_USED];
+#pragma unroll
+    for (int k = 0; k < QE_K_USED; ++k) {
+        float bv = -INFINITY;
+        int bk = 1 << 20, be = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int e = lane + 64 * j, key = (e & 15) * 16 + (e >> 4);
+            if (v[j] > bv || (v[j] == bv && key < bk)) { bv = v[j]; bk = key; be = e; }
+        }
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const float ov = __shfl_xor(bv, off, 64);
+            const int ok = __shfl_xor(bk, off, 64), oe = __shfl_xor(be, off, 64);
+            if (ov > bv || (ov == bv && ok < bk)) { bv = ov; bk = ok; be = oe; }
+        }
+        sel[k] = bv;
+        id[k] = be;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            if (lane + 64 * j == be) v[j] = -INFINITY;
+    }
+    if (lane == 0) {
+        float s = 0.f;
+#pragma unroll
+        for (int k = 0; k < QE_K_USED; ++k) s += expf(sel[k] - sel[0]);
+#pragma unroll
+        for (int k = 0; k < QE_K_USED; ++k) {
+            ids[k] = id[k];
+            wts[k] = expf(sel[k] - sel[0]) / s;
+        }
+        *shg = 1.f / (1.f + expf(-lg_sh));
+    }
+}
+QE_DEV void wave_topk(const float *lg, int lane, int32_t *ids, float *wts, float *shg) {
+    float v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = lg[lane + 64 * j];
+    wave_topk_vals(v, lg[QE_N_EXPERT], lane, ids, wts, shg);
+}
+
+// Exclusive scan of one int per thread over a 256-thread block; returns the
+// exclusive prefix, *total gets the sum.  `tmp` is 256 ints of LDS.
+QE_DEV int block_scan256(int v, int *tmp, int *total) {
+    const int tid = threadIdx.x;
+    tmp[tid] = v;
+    __syncthreads();
+#pragma unroll
+    for (int off = 1; off < 256; off <<= 1) {
+        const int a = tid >= off ? tmp[tid - off] : 0;
+        __syncthreads();
+        tmp[tid] += a;
+        __syncthreads();
+    }
+    const int incl = tmp[tid];
+    *total = tmp[255];
+    __syncthreads();
+    return incl - v;
+}
+
+// One canonical normalisation of a 2048-vector by one wave.  Lane c owns the
+// 32 contiguous elements [32c, 32c+32) in v[]; on return v holds xn.
+QE_DEV void wave_norm_chunk(float v[32], const float *post_norm, int lane) {
+    if (!post_norm) return;
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) ss = fmaf(v[i], v[i], ss);
+    ss = wave_sum_canon(ss);
+    const float inv = 1.0f / sqrtf(ss / (float)QE_D + QE_RMS_EPS);
+    const float4 *wr = (const float4 *)(post_norm + lane * 32);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float4 w = wr[i];
+        v[4 * i + 0] = (v[4 * i + 0] * inv) * w.x;
+        v[4 * i + 1] = (v[4 * i + 1] * inv) * w.y;
+        v[4 * i + 2] = (v[4 * i + 2] * inv) * w.z;
+        v[4 * i + 3] = (v[4 * i + 3] * inv) * w.w;
+    }
+}
+
+// Quantise the 32 values a lane holds (one block) and store int8 + scale.
+QE_DEV void lane_quant_store(const float v[32], int8_t *q_out, float *s_out) {
+    float amax = 0.f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
+    float d;
+    const float id = quant_scale_inv(amax, d);
+    uint32_t w[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        uint32_t x = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) x |= (uint32_t)(uint8_t)quant_one(v[4 * i + j], id) << (8 * j);
+        w[i] = x;
+    }
+    ((uint4 *)q_out)[0] = make_uint4(w[0], w[1], w[2], w[3]);
+    ((uint4 *)q_out)[1] = make_uint4(w[4], w[5], w[6], w[7]);
+    *s_out = d;
+}
+
+QE_DEV void load32(const float *p, float v[32]) {
+    const float4 *q = (const float4 *)p;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float4 t = q[i];
+        v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w;
+    }
+}
+QE_DEV void unpack_i8x32(uint4 a, uint4 b, float w[32]) {
+    const uint32_t d[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) w[4 * i + j] = (float)(int8_t)((d[i] >> (8 * j)) & 0xff);
+}
+

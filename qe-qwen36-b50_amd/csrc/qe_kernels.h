@@ -22,13 +22,30 @@ struct QeLayerPtrs {
 
 // Optional per-kernel event timing (host side): when `on`, every launch of
 // qe_launch_layer is bracketed by two events on its stream.
-enum { QP_ROUTE_SMALL, QP_GU, QP_DOWN_SMALL, QP_NORMQ, QP_ROUTER, QP_SHGU, QP_TOPK, QP_DISPATCH, QP_HQUANT,
-       QP_DOWN_LARGE, QP_SHDN, QP_COMBINE, QP_N };
+enum { QP_DECODE, QP_NORMQ, QP_ROUTER, QP_SHGU, QP_TOPK, QP_DISPATCH, QP_GU, QP_HQUANT, QP_DOWN_LARGE, QP_SHDN,
+       QP_COMBINE, QP_N };
 struct QeProf {
     bool on = false;
     int used = 0, cap = 0, dropped = 0;
     hipEvent_t *ev = nullptr; // 2*cap events
     int *kid = nullptr;       // kernel id per pair
+};
+
+// Event bracket of one launch when per-kernel timing is on.
+struct ProfScope {
+    QeProf *p;
+    hipStream_t st;
+    int slot = -1;
+    ProfScope(QeProf *p_, int kid, hipStream_t s) : p(p_), st(s) {
+        if (!p || !p->on) return;
+        if (p->used >= p->cap) { p->dropped++; return; }
+        slot = p->used++;
+        p->kid[slot] = kid;
+        (void)hipEventRecord(p->ev[2 * slot], st);
+    }
+    ~ProfScope() {
+        if (slot >= 0) (void)hipEventRecord(p->ev[2 * slot + 1], st);
+    }
 };
 
 // Scratch of a context, sized for t_max tokens.
@@ -48,13 +65,6 @@ struct QeScratch {
     QeProf *prof;                           // host-side timing, may be nullptr
 };
 
-struct QeRouteArgs {
-    const float *x; int T; const float *post_norm;
-    const float *router; const float *bias; const uint8_t *sh_gu;
-    float *xn; int8_t *xq; float *xs; float *logits; float *shgu;
-    int32_t *ids; float *wts; float *shg; int32_t *off; int32_t *pairs; int4 *items; int32_t *n_items;
-    uint32_t *counter;
-};
 struct QeExpertArgs {
     const uint8_t *arena; const int8_t *xq; const float *xs;
     const int32_t *pairs; const int4 *items; const int32_t *n_items;
@@ -70,6 +80,25 @@ struct QeDownArgs {
 struct QeGemmArgs {
     const float *A; int T; const float *Bf; const uint8_t *Bq; const float *bias; float *C;
 };
+
+// Persistent decode kernel (qe_decode.hip): T <= QE_SMALL_T tokens through
+// layers first_layer .. first_layer + n_layers - 1 in one cooperative launch.
+struct QeDecodeArgs {
+    const uint8_t *arena; const float *router; const float *bias; const uint8_t *bias_on;
+    const uint8_t *sh_gu; const uint8_t *sh_dn; const float *post_norm;
+    int first_layer, n_layers, T, norm, residual;
+    const float *x_in; float *x_out;
+    // exchange buffers of {value, tag} words (see qe_decode.hip)
+    uint64_t *ex_x;      // 2 x [QE_SMALL_T][2048]
+    uint64_t *ex_logits; // [QE_SMALL_T][257]
+    uint64_t *ex_shgu;   // [QE_SMALL_T][1024]
+    uint64_t *ex_h;      // [QE_SMALL_T*8][512]
+    // routing sink of the last layer (plain stores by workgroup 0)
+    float *logits; int32_t *ids; float *wts; float *shg; int32_t *off; int32_t *pairs; float *sd_out; float *xn_out;
+    unsigned *sync;      // [0] launch epoch, [32] exit counter
+    unsigned *err;       // set to 1 if a poll timed out
+};
+hipError_t qe_launch_decode(const QeDecodeArgs &a, hipStream_t st);
 
 // Launchers (qe_kernels.hip).  xin: layer input; post_norm: nullptr = input is
 // already normalised; x2: residual added to the output or nullptr.

@@ -1,11 +1,7 @@
 // MoE block kernels for gfx950 (wave64).
 //
-// Two launch plans share these kernels (host side in qe_api.hip):
-//  * small T (<= QE_SMALL_T tokens: B=1 decode and the batched verify of
-//    decode_multi<NT>, engine/qe.cpp:1653-1737, 2466-2572): three launches,
-//      k_route_small  norm + router + shared gate|up + (last block) top-8 + dispatch
-//      k_gu           routed gate/up + SwiGLU, weight rows read once per expert
-//      k_down_small   h quantisation + routed down + shared down + combine
+// Launch plans (host side in qe_api.hip):
+//  * small T (<= QE_SMALL_T tokens): the persistent kernel in qe_decode.hip;
 //  * large T (prefill, Engine::moe_batched, engine/qe.cpp:1957-2047):
 //      k_normq, k_gemm_canon (router / shared), k_topk, k_disp_hist,
 //      k_disp_scatter, k_gu, k_hquant, k_down_large, k_combine.
@@ -13,217 +9,6 @@
 // canonical fp32 order exactly; expert products use exact int8 block dots
 // with fp32 block scaling, so they agree with the CPU path to fp32 rounding.
 #include "qe_kernels.h"
-
-// ===========================================================================
-// top-8 of one token by one wave (engine/qe.cpp:1454-1483 semantics):
-// maximum logit first; ties go to the smaller (e % 16, e / 16), the order the
-// reference's 16-lane reduction produces.  Lane l holds e = l + 64 j.
-// ===========================================================================
-QE_DEV void wave_topk(const float *lg, int lane, int32_t *ids, float *wts, float *shg, int *lds_ids = nullptr) {
-    float v[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) v[j] = lg[lane + 64 * j];
-    float sel[QE_K_USED];
-    int id[QE_K_USED];
-#pragma unroll
-    for (int k = 0; k < QE_K_USED; ++k) {
-        float bv = -INFINITY;
-        int bk = 1 << 20, be = 0;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int e = lane + 64 * j, key = (e & 15) * 16 + (e >> 4);
-            if (v[j] > bv || (v[j] == bv && key < bk)) { bv = v[j]; bk = key; be = e; }
-        }
-#pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-            const float ov = __shfl_xor(bv, off, 64);
-            const int ok = __shfl_xor(bk, off, 64), oe = __shfl_xor(be, off, 64);
-            if (ov > bv || (ov == bv && ok < bk)) { bv = ov; bk = ok; be = oe; }
-        }
-        sel[k] = bv;
-        id[k] = be;
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-            if (lane + 64 * j == be) v[j] = -INFINITY;
-    }
-    if (lane == 0) {
-        float s = 0.f;
-#pragma unroll
-        for (int k = 0; k < QE_K_USED; ++k) s += expf(sel[k] - sel[0]);
-#pragma unroll
-        for (int k = 0; k < QE_K_USED; ++k) {
-            ids[k] = id[k];
-            if (lds_ids) lds_ids[k] = id[k];
-            wts[k] = expf(sel[k] - sel[0]) / s;
-        }
-        *shg = 1.f / (1.f + expf(-lg[QE_N_EXPERT]));
-    }
-}
-
-// Exclusive scan of one int per thread over a 256-thread block; returns the
-// exclusive prefix, *total gets the sum.  `tmp` is 256 ints of LDS.
-QE_DEV int block_scan256(int v, int *tmp, int *total) {
-    const int tid = threadIdx.x;
-    tmp[tid] = v;
-    __syncthreads();
-#pragma unroll
-    for (int off = 1; off < 256; off <<= 1) {
-        const int a = tid >= off ? tmp[tid - off] : 0;
-        __syncthreads();
-        tmp[tid] += a;
-        __syncthreads();
-    }
-    const int incl = tmp[tid];
-    *total = tmp[255];
-    __syncthreads();
-    return incl - v;
-}
-
-// One canonical normalisation of a 2048-vector by one wave.  Lane c owns the
-// 32 contiguous elements [32c, 32c+32) in v[]; on return v holds xn.
-QE_DEV void wave_norm_chunk(float v[32], const float *post_norm, int lane) {
-    if (!post_norm) return;
-    float ss = 0.f;
-#pragma unroll
-    for (int i = 0; i < 32; ++i) ss = fmaf(v[i], v[i], ss);
-    ss = wave_sum_canon(ss);
-    const float inv = 1.0f / sqrtf(ss / (float)QE_D + QE_RMS_EPS);
-    const float4 *wr = (const float4 *)(post_norm + lane * 32);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const float4 w = wr[i];
-        v[4 * i + 0] = (v[4 * i + 0] * inv) * w.x;
-        v[4 * i + 1] = (v[4 * i + 1] * inv) * w.y;
-        v[4 * i + 2] = (v[4 * i + 2] * inv) * w.z;
-        v[4 * i + 3] = (v[4 * i + 3] * inv) * w.w;
-    }
-}
-
-// Quantise the 32 values a lane holds (one block) and store int8 + scale.
-QE_DEV void lane_quant_store(const float v[32], int8_t *q_out, float *s_out) {
-    float amax = 0.f;
-#pragma unroll
-    for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
-    float d;
-    const float id = quant_scale_inv(amax, d);
-    uint32_t w[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        uint32_t x = 0;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) x |= (uint32_t)(uint8_t)quant_one(v[4 * i + j], id) << (8 * j);
-        w[i] = x;
-    }
-    ((uint4 *)q_out)[0] = make_uint4(w[0], w[1], w[2], w[3]);
-    ((uint4 *)q_out)[1] = make_uint4(w[4], w[5], w[6], w[7]);
-    *s_out = d;
-}
-
-QE_DEV void load32(const float *p, float v[32]) {
-    const float4 *q = (const float4 *)p;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const float4 t = q[i];
-        v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w;
-    }
-}
-QE_DEV void unpack_i8x32(uint4 a, uint4 b, float w[32]) {
-    const uint32_t d[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) w[4 * i + j] = (float)(int8_t)((d[i] >> (8 * j)) & 0xff);
-}
-
-// ===========================================================================
-// small T, launch 1: norm + router + shared gate|up; the last block to finish
-// does top-8 and the dispatch for all T tokens.
-// grid = ceil((257 + 1024) / 4), block = 256: one wave per weight row.
-// ===========================================================================
-__global__ __launch_bounds__(256) void k_route_small(QeRouteArgs a) {
-    __shared__ float sx[QE_SMALL_T * QE_D]; // sx[t][i][c] = xn[t][32c + i]
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, T = a.T;
-
-    for (int t = wv; t < T; t += 4) {
-        float v[32];
-        load32(a.x + (size_t)t * QE_D + lane * 32, v);
-        wave_norm_chunk(v, a.post_norm, lane);
-#pragma unroll
-        for (int i = 0; i < 32; ++i) sx[t * QE_D + i * 64 + lane] = v[i];
-        if ((int)blockIdx.x == t) {
-            float4 *xo = (float4 *)(a.xn + (size_t)t * QE_D + lane * 32);
-#pragma unroll
-            for (int i = 0; i < 8; ++i) xo[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
-            lane_quant_store(v, a.xq + (size_t)t * QE_D + lane * 32, a.xs + (size_t)t * (QE_D / 32) + lane);
-        }
-    }
-    __syncthreads();
-
-    const int row = blockIdx.x * 4 + wv;
-    if (row < QE_ROUTER_ROWS) {
-        float w[32];
-        load32(a.router + (size_t)row * QE_D + lane * 32, w);
-        const bool add_bias = a.bias && row < QE_N_EXPERT;
-        const float b = add_bias ? a.bias[row] : 0.f;
-        for (int t = 0; t < T; ++t) {
-            float acc = 0.f;
-#pragma unroll
-            for (int i = 0; i < 32; ++i) acc = fmaf(w[i], sx[t * QE_D + i * 64 + lane], acc);
-            acc = wave_sum_canon(acc);
-            if (lane == 0) a.logits[t * QE_ROUTER_ROWS + row] = add_bias ? acc + b : acc;
-        }
-    } else if (row < QE_ROUTER_ROWS + QE_SH_GU_ROWS) {
-        const int r = row - QE_ROUTER_ROWS;
-        const uint8_t *rp = a.sh_gu + (size_t)r * QE_SH_GU_ROW_BYTES;
-        const uint4 q0 = ((const uint4 *)(rp + lane * 32))[0], q1 = ((const uint4 *)(rp + lane * 32))[1];
-        const float sc = f16_bits_to_f32(((const uint16_t *)(rp + QE_D))[lane]);
-        float w[32];
-        unpack_i8x32(q0, q1, w);
-        for (int t = 0; t < T; ++t) {
-            float acc = 0.f;
-#pragma unroll
-            for (int i = 0; i < 32; ++i) acc = fmaf(w[i], sx[t * QE_D + i * 64 + lane], acc);
-            acc = wave_sum_canon(acc * sc);
-            if (lane == 0) a.shgu[t * QE_SH_GU_ROWS + r] = acc;
-        }
-    }
-
-    // ---- last block: top-8 + dispatch ----
-    __threadfence();
-    __syncthreads();
-    int *si = (int *)sx; // reuse LDS
-    if (threadIdx.x == 0) si[0] = (int)atomicAdd(a.counter, 1u);
-    __syncthreads();
-    const bool last = si[0] == (int)gridDim.x - 1;
-    __syncthreads();
-    if (!last) return;
-    __threadfence();
-    int *s_ids = si, *s_scan = si + 64, *s_off = si + 64 + 256;
-    for (int t = wv; t < T; t += 4)
-        wave_topk(a.logits + t * QE_ROUTER_ROWS, lane, a.ids + t * QE_K_USED, a.wts + t * QE_K_USED, a.shg + t,
-                  s_ids + t * QE_K_USED);
-    __syncthreads();
-    const int np = T * QE_K_USED, tid = threadIdx.x;
-    int cnt = 0;
-    for (int p = 0; p < np; ++p) cnt += s_ids[p] == tid;
-    int total;
-    const int off = block_scan256(cnt, s_scan, &total);
-    s_off[tid] = off;
-    a.off[tid] = off;
-    if (tid == 0) a.off[QE_N_EXPERT] = total;
-    int nitems;
-    const int item = block_scan256(cnt > 0 ? 1 : 0, s_scan, &nitems);
-    if (cnt > 0) a.items[item] = make_int4(tid, off, cnt, 0);
-    if (tid == 0) *a.n_items = nitems;
-    __syncthreads();
-    if (tid < np) {
-        const int e = s_ids[tid];
-        int rank = 0;
-        for (int p = 0; p < tid; ++p) rank += s_ids[p] == e;
-        a.pairs[s_off[e] + rank] = tid;
-    }
-    if (tid == 0) atomicExch(a.counter, 0u);
-}
 
 // ===========================================================================
 // routed gate/up + SwiGLU for one work item (expert e, up to TC of its pairs)
@@ -278,76 +63,6 @@ __global__ __launch_bounds__(256) void k_gu(QeExpertArgs a) {
         G = sum16(G);
         U = sum16(U);
         if (l16 == 0) a.h[(size_t)sp[j] * QE_FF_EXP + r] = silu_mul(G, U);
-    }
-}
-
-// ===========================================================================
-// small T, launch 3: quantise h of every pair, routed down + weight, shared
-// expert down on silu(g)*u, combine (engine/qe.cpp:2033-2045 order:
-// x2 + shg*sd, then + y_{t,k} for k = 0..7).  grid = 2048/8, block = 128
-// (2 waves x 4 rows, 16 lanes per row, lane = block of the 512-wide row).
-// ===========================================================================
-__global__ __launch_bounds__(128) void k_down_small(QeDownArgs a) {
-    __shared__ uint4 shq[QE_SMALL_T * QE_K_USED * QE_FF_EXP / 16];
-    __shared__ float shs[QE_SMALL_T * QE_K_USED * (QE_FF_EXP / 32)];
-    __shared__ float shh[QE_SMALL_T * QE_FF_SH];
-    __shared__ float syp[QE_SMALL_T * QE_K_USED * 8];
-    const int T = a.T, np = T * QE_K_USED, tid = threadIdx.x;
-    for (int i = tid; i < np * (QE_FF_EXP / 32); i += 128) {
-        const int p = i / (QE_FF_EXP / 32), b = i % (QE_FF_EXP / 32);
-        float v[32];
-        load32(a.h + (size_t)p * QE_FF_EXP + b * 32, v);
-        lane_quant_store(v, (int8_t *)shq + p * QE_FF_EXP + b * 32, shs + i);
-    }
-    for (int i = tid; i < T * QE_FF_SH; i += 128) {
-        const int t = i / QE_FF_SH, k = i % QE_FF_SH;
-        shh[i] = silu_mul(a.shgu[t * QE_SH_GU_ROWS + k], a.shgu[t * QE_SH_GU_ROWS + QE_FF_SH + k]);
-    }
-    __syncthreads();
-    const int lane = tid & 63, wv = tid >> 6, l16 = lane & 15, rl = wv * 4 + (lane >> 4);
-    const int r = blockIdx.x * 8 + rl;
-    const int nitems = *a.n_items;
-    for (int i = 0; i < nitems; ++i) {
-        const int4 it = a.items[i];
-        const uint8_t *drow = a.arena + (size_t)it.x * QE_EXPERT_BYTES + QE_EXPERT_DOWN_OFF + (size_t)r * QE_DN_ROW_BYTES;
-        const nl4_blk w = nl4_decode_block(*(const uint4 *)(drow + l16 * 16));
-        const float sc = f16_bits_to_f32(((const uint16_t *)(drow + QE_FF_EXP / 2))[l16]);
-        for (int j = 0; j < it.z; ++j) {
-            const int p = a.pairs[it.y + j];
-            const int P = nl4_block_dot(w, shq[p * (QE_FF_EXP / 16) + l16 * 2], shq[p * (QE_FF_EXP / 16) + l16 * 2 + 1]);
-            float v = (sc * shs[p * (QE_FF_EXP / 32) + l16]) * (float)P;
-            v = sum16(v);
-            if (l16 == 0) syp[p * 8 + rl] = a.wts[p] * v;
-        }
-    }
-    // shared down: Q8 row r, lane = block l16
-    const uint8_t *srow = a.sh_dn + (size_t)r * QE_SH_DN_ROW_BYTES;
-    float w8[32];
-    unpack_i8x32(((const uint4 *)(srow + l16 * 32))[0], ((const uint4 *)(srow + l16 * 32))[1], w8);
-    const float ssc = f16_bits_to_f32(((const uint16_t *)(srow + QE_FF_SH))[l16]);
-    float sdv[QE_SMALL_T];
-#pragma unroll
-    for (int t = 0; t < QE_SMALL_T; ++t) {
-        sdv[t] = 0.f;
-        if (t < T) {
-            float acc = 0.f;
-#pragma unroll
-            for (int i = 0; i < 32; ++i) acc = fmaf(w8[i], shh[t * QE_FF_SH + l16 * 32 + i], acc);
-            sdv[t] = sum16(acc * ssc);
-        }
-    }
-    __syncthreads();
-    if (l16 == 0) {
-#pragma unroll
-        for (int t = 0; t < QE_SMALL_T; ++t) {
-            if (t >= T) break;
-            const size_t o = (size_t)t * QE_D + r;
-            float acc = (a.x2 ? a.x2[o] : 0.f) + a.shg[t] * sdv[t];
-#pragma unroll
-            for (int k = 0; k < QE_K_USED; ++k) acc += syp[(t * QE_K_USED + k) * 8 + rl];
-            a.out[o] = acc;
-            a.sd[o] = sdv[t];
-        }
     }
 }
 
@@ -671,22 +386,6 @@ __global__ void k_fill_f32(float *p, float v, int64_t n) {
 // ===========================================================================
 // host launchers
 // ===========================================================================
-// Event bracket of one launch when per-kernel timing is on.
-struct ProfScope {
-    QeProf *p;
-    hipStream_t st;
-    int slot = -1;
-    ProfScope(QeProf *p_, int kid, hipStream_t s) : p(p_), st(s) {
-        if (!p || !p->on) return;
-        if (p->used >= p->cap) { p->dropped++; return; }
-        slot = p->used++;
-        p->kid[slot] = kid;
-        (void)hipEventRecord(p->ev[2 * slot], st);
-    }
-    ~ProfScope() {
-        if (slot >= 0) (void)hipEventRecord(p->ev[2 * slot + 1], st);
-    }
-};
 #define QE_PROF(kid) ProfScope prof_scope_##kid(S.prof, kid, st)
 
 hipError_t qe_launch_layer(const QeLayerPtrs &L, const QeScratch &S, const float *xin, bool norm, const float *x2,
@@ -696,23 +395,6 @@ hipError_t qe_launch_layer(const QeLayerPtrs &L, const QeScratch &S, const float
     QeExpertArgs ea{L.arena, S.xq, S.xs, S.pairs, S.items, S.n_items, S.h};
     QeDownArgs da{L.arena, L.sh_dn, T, S.h, S.hq, S.hs, S.shgu, S.pairs, S.items, S.n_items,
                   S.wts, S.shg, x2, S.yp, S.sd, out};
-    if (T <= QE_SMALL_T) {
-        QeRouteArgs ra{xin, T, pn, L.router, L.bias, L.sh_gu, S.xn, S.xq, S.xs, S.logits, S.shgu,
-                       S.ids, S.wts, S.shg, S.off, S.pairs, S.items, S.n_items, S.counter};
-        {
-            QE_PROF(QP_ROUTE_SMALL);
-            k_route_small<<<(QE_ROUTER_ROWS + QE_SH_GU_ROWS + 3) / 4, 256, 0, st>>>(ra);
-        }
-        {
-            QE_PROF(QP_GU);
-            k_gu<QE_SMALL_T><<<dim3(np < QE_N_EXPERT ? np : QE_N_EXPERT, QE_FF_EXP / 16), 256, 0, st>>>(ea);
-        }
-        {
-            QE_PROF(QP_DOWN_SMALL);
-            k_down_small<<<QE_D / 8, 128, 0, st>>>(da);
-        }
-        return hipGetLastError();
-    }
     const int mt = (T + 63) / 64;
     {
         QE_PROF(QP_NORMQ);

@@ -31,7 +31,7 @@ EXPERT_BYTES = 1769472
 SH_GU_BYTES = 1024 * 2176
 SH_DN_BYTES = 2048 * 544
 
-NPROF = 12
+NPROF = 11
 QE_OK, QE_ERR_ARG, QE_ERR_HIP, QE_ERR_OOM, QE_ERR_STATE = 0, -1, -2, -3, -4
 
 
