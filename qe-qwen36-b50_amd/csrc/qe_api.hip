@@ -122,8 +122,7 @@ int qe_moe_create(int device, int n_layers, int t_max, qe_moe_ctx **out) {
     A(S.chunk_hist, nch * QE_N_EXPERT * 4);
     A(S.counter, 256);
     A(c->bias_on, L);
-    A(c->ex, (size_t)(2 * QE_SMALL_T * QE_D + QE_SMALL_T * QE_ROUTER_ROWS + QE_SMALL_T * QE_SH_GU_ROWS +
-                      QE_SMALL_T * QE_K_USED * QE_FF_EXP) * 8);
+    A(c->ex, (size_t)QE_DECODE_EX_WORDS * 8);
     A(c->sync, 8192);
     A(c->err, 256);
     A(c->pingpong[0], T * QE_D * 4);
@@ -139,8 +138,7 @@ int qe_moe_create(int device, int n_layers, int t_max, qe_moe_ctx **out) {
     if (hipMemset(S.counter, 0, 256) != hipSuccess || hipMemset(c->bias, 0, L * QE_N_EXPERT * 4) != hipSuccess ||
         hipMemset(c->bias_on, 0, L) != hipSuccess || hipMemset(c->sync, 0, 8192) != hipSuccess ||
         hipMemset(c->err, 0, 256) != hipSuccess ||
-        hipMemset(c->ex, 0, (size_t)(2 * QE_SMALL_T * QE_D + QE_SMALL_T * QE_ROUTER_ROWS + QE_SMALL_T * QE_SH_GU_ROWS +
-                                     QE_SMALL_T * QE_K_USED * QE_FF_EXP) * 8) != hipSuccess ||
+        hipMemset(c->ex, 0, (size_t)QE_DECODE_EX_WORDS * 8) != hipSuccess ||
         hipDeviceSynchronize() != hipSuccess) {
         free_all(c);
         delete c;
@@ -210,10 +208,7 @@ static hipError_t run_decode(qe_moe_ctx *c, int first, int n, const float *in, f
     d.sh_gu = c->sh_gu; d.sh_dn = c->sh_dn; d.post_norm = c->post_norm;
     d.first_layer = first; d.n_layers = n; d.T = T; d.norm = norm_res; d.residual = norm_res;
     d.x_in = in; d.x_out = out;
-    d.ex_x = c->ex;
-    d.ex_logits = d.ex_x + 2 * QE_SMALL_T * QE_D;
-    d.ex_shgu = d.ex_logits + QE_SMALL_T * QE_ROUTER_ROWS;
-    d.ex_h = d.ex_shgu + QE_SMALL_T * QE_SH_GU_ROWS;
+    d.ex = c->ex;
     d.logits = c->S.logits; d.ids = c->S.ids; d.wts = c->S.wts; d.shg = c->S.shg; d.off = c->S.off; d.pairs = c->S.pairs;
     d.sd_out = c->S.sd; d.xn_out = c->S.xn;
     d.sync = c->sync; d.err = c->err;

@@ -88,17 +88,14 @@ struct QeDecodeArgs {
     const uint8_t *sh_gu; const uint8_t *sh_dn; const float *post_norm;
     int first_layer, n_layers, T, norm, residual;
     const float *x_in; float *x_out;
-    // exchange buffers of {value, tag} words (see qe_decode.hip)
-    uint64_t *ex_x;      // 2 x [QE_SMALL_T][2048]
-    uint64_t *ex_logits; // [QE_SMALL_T][257]
-    uint64_t *ex_shgu;   // [QE_SMALL_T][1024]
-    uint64_t *ex_h;      // [QE_SMALL_T*8][512]
+    uint64_t *ex;        // exchange words {value, tag}, QE_DECODE_EX_WORDS of them (qe_decode.hip)
     // routing sink of the last layer (plain stores by workgroup 0)
     float *logits; int32_t *ids; float *wts; float *shg; int32_t *off; int32_t *pairs; float *sd_out; float *xn_out;
-    unsigned *sync;      // [0] launch epoch, [32] exit counter
+    unsigned *sync;      // [0] launch epoch, [32] exit counter, [64..832) stage flags
     unsigned *err;       // set to 1 if a poll timed out
 };
 hipError_t qe_launch_decode(const QeDecodeArgs &a, hipStream_t st);
+#define QE_DECODE_EX_WORDS (2 * QE_SMALL_T * QE_D + QE_SMALL_T * QE_ROUTER_ROWS + QE_SMALL_T * QE_FF_SH + QE_SMALL_T * 8 * 16 * 9)
 
 // Launchers (qe_kernels.hip).  xin: layer input; post_norm: nullptr = input is
 // already normalised; x2: residual added to the output or nullptr.
