@@ -189,12 +189,19 @@ def main():
             mp.forward_normed(0, xp, yp, 512, stream=torch.cuda.current_stream())
         pms = timed(torch, lambda: mp.forward_normed(0, xp, yp, 512, stream=torch.cuda.current_stream()),
                     max(5, args.steps // 10), torch.cuda.current_stream())
+        mp.profile(True)
+        for _ in range(5):
+            mp.forward_normed(0, xp, yp, 512, stream=torch.cuda.current_stream())
+        torch.cuda.synchronize()
+        pk = mp.profile_read()
+        mp.profile(False)
         r = mp.routing(512)
         cnt = np.diff(r["off"])
         pre = {"prefill512_ms": round(pms, 4), "prefill512_tflops": round(512 * FLOP_PER_TOKEN / (pms / 1e3) / 1e12, 3),
                "prefill512_routing": {"distinct_experts": int(np.count_nonzero(cnt)), "max_tokens_per_expert": int(cnt.max()),
                                       "top8_share": round(float(np.sort(cnt)[-8:].sum() / cnt.sum()), 4),
-                                      "experts_lt4_tokens": int(((cnt > 0) & (cnt < 4)).sum())}}
+                                      "experts_lt4_tokens": int(((cnt > 0) & (cnt < 4)).sum())},
+               "prefill512_kernels_us": {k: round(v[0] / v[1] * 1e3, 2) for k, v in pk.items()}}
         del mp
 
     # ---------------- CPU baseline ----------------

@@ -90,7 +90,7 @@ int qe_moe_create(int device, int n_layers, int t_max, qe_moe_ctx **out) {
     c->has_bias.assign(n_layers, 0);
     c->ready.assign(n_layers, 0);
     const size_t L = (size_t)n_layers, T = (size_t)t_max, NP = T * QE_K_USED;
-    const size_t max_items = NP / QE_LARGE_TC + QE_N_EXPERT;
+    const size_t max_items = NP / QE_MFMA_MC + QE_N_EXPERT;
     const size_t nch = (NP + 1023) / 1024;
     int rc = QE_OK;
     QeScratch &S = c->S;
@@ -103,10 +103,11 @@ int qe_moe_create(int device, int n_layers, int t_max, qe_moe_ctx **out) {
     A(c->sh_dn, L * QE_SH_DN_BYTES);
     A(c->post_norm, L * QE_D * 4);
     A(S.xn, T * QE_D * 4);
-    A(S.xq, T * QE_D);
+    A(S.xqp, T * QE_D);
     A(S.xs, T * (QE_D / 32) * 4);
     A(S.logits, T * QE_ROUTER_ROWS * 4);
     A(S.shgu, T * QE_SH_GU_ROWS * 4);
+    A(S.rpart, 4 * T * QE_ROUTER_ROWS * 4);
     A(S.ids, NP * 4);
     A(S.wts, NP * 4);
     A(S.shg, T * 4);
@@ -114,8 +115,7 @@ int qe_moe_create(int device, int n_layers, int t_max, qe_moe_ctx **out) {
     A(S.pairs, NP * 4);
     A(S.items, max_items * sizeof(int4));
     A(S.n_items, 4);
-    A(S.h, NP * QE_FF_EXP * 4);
-    A(S.hq, NP * QE_FF_EXP);
+    A(S.hqp, NP * QE_FF_EXP);
     A(S.hs, NP * (QE_FF_EXP / 32) * 4);
     A(S.sd, T * QE_D * 4);
     A(S.yp, NP * QE_D * 4);
@@ -293,8 +293,9 @@ int qe_moe_get_logits(qe_moe_ctx *c, int T, float *logits, void *stream) {
 }
 
 static const char *const k_prof_names[QP_N] = {
-    "k_decode", "k_normq", "k_gemm_canon<router>", "k_gemm_canon<shared_gu>", "k_topk", "k_disp_hist+k_disp_scatter",
-    "k_gu", "k_hquant", "k_down_large", "k_gemm_canon<shared_down>", "k_combine"};
+    "k_decode", "k_normq", "k_router_split+k_router_combine", "k_shared_mfma<gate_up>", "k_topk",
+    "k_disp_hist+k_disp_scatter", "k_expert_mfma<gate_up>+k_expert_mfma<down>", "unused", "unused",
+    "k_shared_mfma<down>", "k_combine"};
 
 int qe_moe_profile(qe_moe_ctx *c, int enable) {
     if (!c) return fail(QE_ERR_ARG, "profile: bad argument");

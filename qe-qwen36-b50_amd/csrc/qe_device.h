@@ -204,6 +204,35 @@ QE_DEV void lane_quant_store(const float v[32], int8_t *q_out, float *s_out) {
     *s_out = d;
 }
 
+// Operand layout of int8 activation rows for the prefill MFMA GEMMs: per pair
+// of 32-blocks (2q, 2q+1), 64 bytes = 4 groups g of 16 bytes; group g holds
+// 8 bytes of block 2q then 8 of block 2q+1, each run being elements
+// 4g..4g+3 followed by 16+4g..16+4g+3 of its block.
+QE_HD inline int qe_opnd_off(int k) {
+    const int b = k >> 5, e = k & 31;
+    return (b >> 1) * 64 + ((e & 15) >> 2) * 16 + (b & 1) * 8 + (e >> 4) * 4 + (e & 3);
+}
+// quantise block b = lane of a row (as lane_quant_store) into the operand layout
+QE_DEV void lane_quant_store_opnd(const float v[32], int8_t *row, int b, float *s_out) {
+    float amax = 0.f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
+    float d;
+    const float id = quant_scale_inv(amax, d);
+    uint32_t w[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        uint32_t x = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) x |= (uint32_t)(uint8_t)quant_one(v[4 * i + j], id) << (8 * j);
+        w[i] = x; // elements 4i..4i+3
+    }
+    int8_t *dst = row + (b >> 1) * 64 + (b & 1) * 8;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) *(uint2 *)(dst + 16 * g) = make_uint2(w[g], w[4 + g]);
+    *s_out = d;
+}
+
 QE_DEV void load32(const float *p, float v[32]) {
     const float4 *q = (const float4 *)p;
 #pragma unroll

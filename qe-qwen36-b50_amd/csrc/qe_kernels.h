@@ -6,9 +6,8 @@
 #include "qe_device.h"
 
 #define QE_SMALL_T 8   /* tokens per call handled by the 3-launch small-T plan */
-#define QE_LARGE_TC 16 /* pairs per work item in the large-T plan */
+#define QE_MFMA_MC 32 /* pairs per work item of the prefill MFMA grouped GEMMs (two 16-row tiles) */
 
-enum { GEMM_ROUTER = 0, GEMM_SHGU = 1, GEMM_SHDN = 2 };
 
 // One layer's weights inside the context.
 struct QeLayerPtrs {
@@ -50,13 +49,14 @@ struct ProfScope {
 
 // Scratch of a context, sized for t_max tokens.
 struct QeScratch {
-    float *xn; int8_t *xq; float *xs;       // [T][2048], [T][2048], [T][64]
+    float *xn; int8_t *xqp; float *xs;      // [T][2048] normed x, its int8 quantisation (operand layout), [T][64] scales
     float *logits;                          // [T][257]
-    float *shgu;                            // [T][1024]
+    float *shgu;                            // [T][1024] (decode: unused) / [T][512] shared silu(g)*u (prefill)
+    float *rpart;                           // [4][T][257] router subtree partials
     int32_t *ids; float *wts; float *shg;   // [T][8], [T][8], [T]
     int32_t *off; int32_t *pairs;           // [257], [T*8]
     int4 *items; int32_t *n_items;          // work items (expert, first pair, count)
-    float *h; int8_t *hq; float *hs;        // [T*8][512], [T*8][512], [T*8][16]
+    int8_t *hqp; float *hs;                 // [T*8][512] quantised h (operand layout), [T*8][16] scales
     float *sd;                              // [T][2048] shared-expert output
     float *yp;                              // [T*8][2048] weighted expert outputs
     int32_t *chunk_hist;                    // [T*8/1024][256]
@@ -65,20 +65,10 @@ struct QeScratch {
     QeProf *prof;                           // host-side timing, may be nullptr
 };
 
-struct QeExpertArgs {
-    const uint8_t *arena; const int8_t *xq; const float *xs;
-    const int32_t *pairs; const int4 *items; const int32_t *n_items;
-    float *h;
-};
-struct QeDownArgs {
-    const uint8_t *arena; const uint8_t *sh_dn; int T;
-    const float *h; const int8_t *hq; const float *hs; const float *shgu;
-    const int32_t *pairs; const int4 *items; const int32_t *n_items;
-    const float *wts; const float *shg; const float *x2;
-    float *yp; float *sd; float *out;
-};
-struct QeGemmArgs {
-    const float *A; int T; const float *Bf; const uint8_t *Bq; const float *bias; float *C;
+struct QeCombineArgs {
+    int T;
+    const float *yp; const float *sd; const float *shg; const float *x2;
+    float *out;
 };
 
 // Persistent decode kernel (qe_decode.hip): T <= QE_SMALL_T tokens through
@@ -102,6 +92,8 @@ hipError_t qe_launch_decode(const QeDecodeArgs &a, hipStream_t st);
 hipError_t qe_launch_layer(const QeLayerPtrs &L, const QeScratch &S, const float *xin, bool norm, const float *x2,
                            float *out, int T, hipStream_t st);
 hipError_t qe_launch_dispatch(const QeScratch &S, int T, hipStream_t st);
+hipError_t qe_launch_expert_mfma(const QeLayerPtrs &L, const QeScratch &S, int T, hipStream_t st);
+hipError_t qe_launch_shared_mfma(const QeLayerPtrs &L, const QeScratch &S, int T, bool gate_up, hipStream_t st);
 hipError_t qe_launch_synth_layer(uint8_t *arena_l, float *router_l, uint8_t *sh_gu_l, uint8_t *sh_dn_l,
                                  float *post_norm_l, uint64_t seed, int layer, hipStream_t st);
 hipError_t qe_launch_synth_x(float *out, uint64_t seed, int inst, int64_t n, hipStream_t st);

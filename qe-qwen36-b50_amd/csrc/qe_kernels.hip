@@ -3,74 +3,19 @@
 // Launch plans (host side in qe_api.hip):
 //  * small T (<= QE_SMALL_T tokens): the persistent kernel in qe_decode.hip;
 //  * large T (prefill, Engine::moe_batched, engine/qe.cpp:1957-2047):
-//      k_normq, k_gemm_canon (router / shared), k_topk, k_disp_hist,
-//      k_disp_scatter, k_gu, k_hquant, k_down_large, k_combine.
+//      k_normq, k_router_split + k_router_combine, the shared-expert MFMA
+//      GEMMs and the routed-expert MFMA grouped GEMMs of qe_prefill.hip,
+//      k_topk, k_disp_hist, k_disp_scatter, k_combine.
 // Routing (RMSNorm, router dot products, top-8) follows the checker's
 // canonical fp32 order exactly; expert products use exact int8 block dots
 // with fp32 block scaling, so they agree with the CPU path to fp32 rounding.
 #include "qe_kernels.h"
 
 // ===========================================================================
-// routed gate/up + SwiGLU for one work item (expert e, up to TC of its pairs)
-// and 16 rows.  grid = (items, 32 row groups), block = 256 (4 waves x 4 rows;
-// 16 lanes per row, lane owns blocks l16 + 16 j).  Weight rows are read and
-// decoded once, then dotted with every token of the item.
-// h[p][r] = silu(g) * u in fp32 (engine/qe.cpp:2066-2072).
-// ===========================================================================
-template <int TC>
-__global__ __launch_bounds__(256) void k_gu(QeExpertArgs a) {
-    __shared__ uint4 sxq[TC * QE_D / 16];
-    __shared__ float sxs[TC * (QE_D / 32)];
-    __shared__ int sp[TC];
-    if ((int)blockIdx.x >= *a.n_items) return;
-    const int4 it = a.items[blockIdx.x];
-    const int e = it.x, start = it.y, n = it.z, tid = threadIdx.x;
-    if (tid < n) sp[tid] = a.pairs[start + tid];
-    __syncthreads();
-    for (int i = tid; i < n * (QE_D / 16); i += 256) {
-        const int j = i / (QE_D / 16), part = i % (QE_D / 16);
-        sxq[i] = ((const uint4 *)(a.xq + (size_t)(sp[j] / QE_K_USED) * QE_D))[part];
-    }
-    for (int i = tid; i < n * (QE_D / 32); i += 256) {
-        const int j = i / (QE_D / 32), b = i % (QE_D / 32);
-        sxs[i] = a.xs[(size_t)(sp[j] / QE_K_USED) * (QE_D / 32) + b];
-    }
-    const int lane = tid & 63, wv = tid >> 6, l16 = lane & 15;
-    const int r = blockIdx.y * 16 + wv * 4 + (lane >> 4);
-    const uint8_t *base = a.arena + (size_t)e * QE_EXPERT_BYTES;
-    const uint8_t *rg = base + (size_t)r * QE_GU_ROW_BYTES, *ru = base + (size_t)(QE_FF_EXP + r) * QE_GU_ROW_BYTES;
-    nl4_blk dg[4], du[4];
-    float sg[4], su[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int b = l16 + 16 * j;
-        dg[j] = nl4_decode_block(*(const uint4 *)(rg + b * 16));
-        du[j] = nl4_decode_block(*(const uint4 *)(ru + b * 16));
-        sg[j] = f16_bits_to_f32(((const uint16_t *)(rg + QE_D / 2))[b]);
-        su[j] = f16_bits_to_f32(((const uint16_t *)(ru + QE_D / 2))[b]);
-    }
-    __syncthreads();
-    for (int j = 0; j < n; ++j) {
-        float G = 0.f, U = 0.f;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const int b = l16 + 16 * q;
-            const uint4 x0 = sxq[j * (QE_D / 16) + b * 2], x1 = sxq[j * (QE_D / 16) + b * 2 + 1];
-            const float xsv = sxs[j * (QE_D / 32) + b];
-            G = fmaf(sg[q] * xsv, (float)nl4_block_dot(dg[q], x0, x1), G);
-            U = fmaf(su[q] * xsv, (float)nl4_block_dot(du[q], x0, x1), U);
-        }
-        G = sum16(G);
-        U = sum16(U);
-        if (l16 == 0) a.h[(size_t)sp[j] * QE_FF_EXP + r] = silu_mul(G, U);
-    }
-}
-
-// ===========================================================================
 // large T kernels
 // ===========================================================================
 // wave per token: xn, xq, xs
-__global__ __launch_bounds__(256) void k_normq(const float *x, int T, const float *post_norm, float *xn, int8_t *xq,
+__global__ __launch_bounds__(256) void k_normq(const float *x, int T, const float *post_norm, float *xn, int8_t *xqp,
                                                float *xs) {
     const int lane = threadIdx.x & 63, t = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (t >= T) return;
@@ -80,42 +25,33 @@ __global__ __launch_bounds__(256) void k_normq(const float *x, int T, const floa
     float4 *xo = (float4 *)(xn + (size_t)t * QE_D + lane * 32);
 #pragma unroll
     for (int i = 0; i < 8; ++i) xo[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
-    lane_quant_store(v, xq + (size_t)t * QE_D + lane * 32, xs + (size_t)t * (QE_D / 32) + lane);
+    lane_quant_store_opnd(v, xqp + (size_t)t * QE_D, lane, xs + (size_t)t * (QE_D / 32) + lane);
 }
 
-// Tiled fp32 GEMM C[m][n] = sum_k A[m][k] B[n][k] in the canonical order:
-// per 32-wide k chunk an fma chain from 0, chunk sums merged by the pairwise
-// tree (chunks (c, c+1), then pairs of pairs, ...).  Tile 64 x 64, 256
-// threads, 4 x 4 outputs per thread.
-//   GEMM_ROUTER: A = xn [T][2048], B = fp32 rows [257][2048], C = logits (+ bias)
-//   GEMM_SHGU:   A = xn, B = Q8 rows [1024][2048], C = shgu [T][1024]
-//   GEMM_SHDN:   A = silu(g)*u from shgu, K = 512, B = Q8 rows [2048][512], C = sd
-template <int MODE>
-__global__ __launch_bounds__(256) void k_gemm_canon(QeGemmArgs a) {
-    constexpr int KD = MODE == GEMM_SHDN ? QE_FF_SH : QE_D;
-    constexpr int NCH = KD / 32;
-    constexpr int NROWS = MODE == GEMM_ROUTER ? QE_ROUTER_ROWS : (MODE == GEMM_SHGU ? QE_SH_GU_ROWS : QE_D);
+// Router logits in the canonical fp32 order, tiled: C[m][n] = sum_k xn[m][k] W[n][k].
+// Canonical order: per 32-wide k chunk an fma chain from 0, chunk sums merged by
+// the pairwise tree (chunks (c, c+1), then pairs of pairs, ...).  The K range is
+// split four ways along that tree: split z computes the 16-chunk subtree
+// [16z, 16z+16) exactly, and k_router_combine forms (s0 + s1) + (s2 + s3), the
+// tree's top two levels -- bit-identical to the unsplit order, with 4x the
+// workgroups.  Tile 64 x 64, 256 threads, 4 x 4 outputs per thread.
+__global__ __launch_bounds__(256) void k_router_split(const float *xn, int T, const float *W, float *part) {
+    constexpr int NCH = 16; // chunks per split
     __shared__ float As[32][68];
     __shared__ float Bs[32][68];
     const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
-    const int m0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
+    const int m0 = blockIdx.y * 64, n0 = blockIdx.x * 64, z = blockIdx.z;
     const int lr = tid >> 2, lk = (tid & 3) * 8; // loader: row lr of the tile, 8 k values
-    float st[7][4][4];
-    for (int c = 0; c < NCH; ++c) {
-        // ---- load A tile: rows m0+lr, k = c*32 + lk .. +7, stored transposed ----
+    float st[5][4][4];
+    for (int cl = 0; cl < NCH; ++cl) {
+        const int c = z * NCH + cl;
         {
             const int m = m0 + lr;
             float v[8];
-            if (m < a.T) {
-                if (MODE == GEMM_SHDN) {
-                    const float *g = a.A + (size_t)m * QE_SH_GU_ROWS + c * 32 + lk;
-#pragma unroll
-                    for (int i = 0; i < 8; ++i) v[i] = silu_mul(g[i], g[QE_FF_SH + i]);
-                } else {
-                    const float4 *p = (const float4 *)(a.A + (size_t)m * QE_D + c * 32 + lk);
-                    const float4 p0 = p[0], p1 = p[1];
-                    v[0] = p0.x; v[1] = p0.y; v[2] = p0.z; v[3] = p0.w; v[4] = p1.x; v[5] = p1.y; v[6] = p1.z; v[7] = p1.w;
-                }
+            if (m < T) {
+                const float4 *p = (const float4 *)(xn + (size_t)m * QE_D + c * 32 + lk);
+                const float4 p0 = p[0], p1 = p[1];
+                v[0] = p0.x; v[1] = p0.y; v[2] = p0.z; v[3] = p0.w; v[4] = p1.x; v[5] = p1.y; v[6] = p1.z; v[7] = p1.w;
             } else {
 #pragma unroll
                 for (int i = 0; i < 8; ++i) v[i] = 0.f;
@@ -123,26 +59,13 @@ __global__ __launch_bounds__(256) void k_gemm_canon(QeGemmArgs a) {
 #pragma unroll
             for (int i = 0; i < 8; ++i) As[lk + i][lr] = v[i];
         }
-        // ---- load B tile ----
         {
             const int n = n0 + lr;
             float v[8];
-            if (n < NROWS) {
-                if (MODE == GEMM_ROUTER) {
-                    const float4 *p = (const float4 *)(a.Bf + (size_t)n * QE_D + c * 32 + lk);
-                    const float4 p0 = p[0], p1 = p[1];
-                    v[0] = p0.x; v[1] = p0.y; v[2] = p0.z; v[3] = p0.w; v[4] = p1.x; v[5] = p1.y; v[6] = p1.z; v[7] = p1.w;
-                } else {
-                    const size_t rb = (size_t)KD + KD / 32 * 2;
-                    const uint8_t *row = a.Bq + (size_t)n * rb;
-                    const uint2 q = *(const uint2 *)(row + c * 32 + lk);
-                    const float sc = f16_bits_to_f32(((const uint16_t *)(row + KD))[c]);
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        v[i] = (float)(int8_t)((q.x >> (8 * i)) & 0xff) * sc;
-                        v[4 + i] = (float)(int8_t)((q.y >> (8 * i)) & 0xff) * sc;
-                    }
-                }
+            if (n < QE_ROUTER_ROWS) {
+                const float4 *p = (const float4 *)(W + (size_t)n * QE_D + c * 32 + lk);
+                const float4 p0 = p[0], p1 = p[1];
+                v[0] = p0.x; v[1] = p0.y; v[2] = p0.z; v[3] = p0.w; v[4] = p1.x; v[5] = p1.y; v[6] = p1.z; v[7] = p1.w;
             } else {
 #pragma unroll
                 for (int i = 0; i < 8; ++i) v[i] = 0.f;
@@ -167,12 +90,11 @@ __global__ __launch_bounds__(256) void k_gemm_canon(QeGemmArgs a) {
                 for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(ar[i], br[j], acc[i][j]);
         }
         __syncthreads();
-        // ---- pairwise-tree merge of this chunk ----
-        bool carry = true;
+        bool carry = true; // pairwise-tree merge of chunk cl
 #pragma unroll
-        for (int l = 0; l < 7; ++l) {
+        for (int l = 0; l < 5; ++l) {
             if (carry) {
-                if (c & (1 << l)) {
+                if (cl & (1 << l)) {
 #pragma unroll
                     for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -187,21 +109,25 @@ __global__ __launch_bounds__(256) void k_gemm_canon(QeGemmArgs a) {
             }
         }
     }
-    constexpr int LV = NCH == 64 ? 6 : (NCH == 16 ? 4 : -1);
-    static_assert(LV >= 0, "chunk count must be 16 or 64");
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int m = m0 + ty * 4 + i;
-        if (m >= a.T) continue;
+        if (m >= T) continue;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int n = n0 + tx * 4 + j;
-            if (n >= NROWS) continue;
-            float v = st[LV][i][j];
-            if (MODE == GEMM_ROUTER && a.bias && n < QE_N_EXPERT) v = v + a.bias[n];
-            a.C[(size_t)m * NROWS + n] = v;
+            if (n < QE_ROUTER_ROWS) part[((size_t)z * T + m) * QE_ROUTER_ROWS + n] = st[4][i][j];
         }
     }
+}
+
+__global__ __launch_bounds__(256) void k_router_combine(const float *part, int T, const float *bias, float *logits) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x, n = (size_t)T * QE_ROUTER_ROWS;
+    if (i >= n) return;
+    const int e = (int)(i % QE_ROUTER_ROWS);
+    float v = (part[i] + part[n + i]) + (part[2 * n + i] + part[3 * n + i]);
+    if (bias && e < QE_N_EXPERT) v = v + bias[e];
+    logits[i] = v;
 }
 
 __global__ __launch_bounds__(256) void k_topk(const float *logits, int T, int32_t *ids, float *wts, float *shg) {
@@ -298,55 +224,8 @@ __global__ __launch_bounds__(1024) void k_disp_scatter(const int32_t *ids, int n
     }
 }
 
-// h -> per-32 int8 + fp32 scale, one thread per (pair, block).
-__global__ __launch_bounds__(256) void k_hquant(const float *h, int nblk, int8_t *hq, float *hs) {
-    const int i = blockIdx.x * 256 + threadIdx.x;
-    if (i >= nblk) return;
-    float v[32];
-    load32(h + (size_t)i * 32, v);
-    lane_quant_store(v, hq + (size_t)i * 32, hs + i);
-}
-
-// routed down for one item and 64 rows: yp[p][r] = w_p * dot(D_e[r], hq_p).
-// grid = (items, 2048/64), block = 256 (4 waves x 4 rows x 4 passes).
-template <int TC>
-__global__ __launch_bounds__(256) void k_down_large(QeDownArgs a) {
-    __shared__ uint4 shq[TC * QE_FF_EXP / 16];
-    __shared__ float shs[TC * (QE_FF_EXP / 32)];
-    __shared__ int sp[TC];
-    if ((int)blockIdx.x >= *a.n_items) return;
-    const int4 it = a.items[blockIdx.x];
-    const int n = it.z, tid = threadIdx.x;
-    if (tid < n) sp[tid] = a.pairs[it.y + tid];
-    __syncthreads();
-    for (int i = tid; i < n * (QE_FF_EXP / 16); i += 256) {
-        const int j = i / (QE_FF_EXP / 16), part = i % (QE_FF_EXP / 16);
-        shq[i] = ((const uint4 *)(a.hq + (size_t)sp[j] * QE_FF_EXP))[part];
-    }
-    for (int i = tid; i < n * (QE_FF_EXP / 32); i += 256) {
-        const int j = i / (QE_FF_EXP / 32), b = i % (QE_FF_EXP / 32);
-        shs[i] = a.hs[(size_t)sp[j] * (QE_FF_EXP / 32) + b];
-    }
-    __syncthreads();
-    const int lane = tid & 63, wv = tid >> 6, l16 = lane & 15;
-    const uint8_t *dbase = a.arena + (size_t)it.x * QE_EXPERT_BYTES + QE_EXPERT_DOWN_OFF;
-#pragma unroll 1
-    for (int pass = 0; pass < 4; ++pass) {
-        const int r = blockIdx.y * 64 + pass * 16 + wv * 4 + (lane >> 4);
-        const uint8_t *drow = dbase + (size_t)r * QE_DN_ROW_BYTES;
-        const nl4_blk w = nl4_decode_block(*(const uint4 *)(drow + l16 * 16));
-        const float sc = f16_bits_to_f32(((const uint16_t *)(drow + QE_FF_EXP / 2))[l16]);
-        for (int j = 0; j < n; ++j) {
-            const int P = nl4_block_dot(w, shq[j * (QE_FF_EXP / 16) + l16 * 2], shq[j * (QE_FF_EXP / 16) + l16 * 2 + 1]);
-            float v = (sc * shs[j * (QE_FF_EXP / 32) + l16]) * (float)P;
-            v = sum16(v);
-            if (l16 == 0) a.yp[(size_t)sp[j] * QE_D + r] = a.wts[sp[j]] * v;
-        }
-    }
-}
-
 // out[t][r] = x2 + shg*sd + sum_k yp[t*8+k][r]  (engine/qe.cpp:2036-2044)
-__global__ __launch_bounds__(256) void k_combine(QeDownArgs a) {
+__global__ __launch_bounds__(256) void k_combine(QeCombineArgs a) {
     const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= (size_t)a.T * QE_D) return;
     const int t = (int)(i / QE_D), r = (int)(i % QE_D);
@@ -391,24 +270,21 @@ __global__ void k_fill_f32(float *p, float v, int64_t n) {
 hipError_t qe_launch_layer(const QeLayerPtrs &L, const QeScratch &S, const float *xin, bool norm, const float *x2,
                            float *out, int T, hipStream_t st) {
     const float *pn = norm ? L.post_norm : nullptr;
-    const int np = T * QE_K_USED;
-    QeExpertArgs ea{L.arena, S.xq, S.xs, S.pairs, S.items, S.n_items, S.h};
-    QeDownArgs da{L.arena, L.sh_dn, T, S.h, S.hq, S.hs, S.shgu, S.pairs, S.items, S.n_items,
-                  S.wts, S.shg, x2, S.yp, S.sd, out};
+    QeCombineArgs da{T, S.yp, S.sd, S.shg, x2, out};
     const int mt = (T + 63) / 64;
     {
         QE_PROF(QP_NORMQ);
-        k_normq<<<(T + 3) / 4, 256, 0, st>>>(xin, T, pn, S.xn, S.xq, S.xs);
+        k_normq<<<(T + 3) / 4, 256, 0, st>>>(xin, T, pn, S.xn, S.xqp, S.xs);
     }
     {
         QE_PROF(QP_ROUTER);
-        k_gemm_canon<GEMM_ROUTER><<<dim3((QE_ROUTER_ROWS + 63) / 64, mt), 256, 0, st>>>(
-            QeGemmArgs{S.xn, T, L.router, nullptr, L.bias, S.logits});
+        k_router_split<<<dim3((QE_ROUTER_ROWS + 63) / 64, mt, 4), 256, 0, st>>>(S.xn, T, L.router, S.rpart);
+        k_router_combine<<<(unsigned)(((size_t)T * QE_ROUTER_ROWS + 255) / 256), 256, 0, st>>>(S.rpart, T, L.bias,
+                                                                                            S.logits);
     }
     {
         QE_PROF(QP_SHGU);
-        k_gemm_canon<GEMM_SHGU><<<dim3(QE_SH_GU_ROWS / 64, mt), 256, 0, st>>>(
-            QeGemmArgs{S.xn, T, nullptr, L.sh_gu, nullptr, S.shgu});
+        (void)qe_launch_shared_mfma(L, S, T, true, st);
     }
     {
         QE_PROF(QP_TOPK);
@@ -418,23 +294,13 @@ hipError_t qe_launch_layer(const QeLayerPtrs &L, const QeScratch &S, const float
         QE_PROF(QP_DISPATCH);
         (void)qe_launch_dispatch(S, T, st);
     }
-    const int max_items = np / QE_LARGE_TC + QE_N_EXPERT;
     {
         QE_PROF(QP_GU);
-        k_gu<QE_LARGE_TC><<<dim3(max_items, QE_FF_EXP / 16), 256, 0, st>>>(ea);
-    }
-    {
-        QE_PROF(QP_HQUANT);
-        k_hquant<<<(np * (QE_FF_EXP / 32) + 255) / 256, 256, 0, st>>>(S.h, np * (QE_FF_EXP / 32), S.hq, S.hs);
-    }
-    {
-        QE_PROF(QP_DOWN_LARGE);
-        k_down_large<QE_LARGE_TC><<<dim3(max_items, QE_D / 64), 256, 0, st>>>(da);
+        (void)qe_launch_expert_mfma(L, S, T, st);
     }
     {
         QE_PROF(QP_SHDN);
-        k_gemm_canon<GEMM_SHDN><<<dim3(QE_D / 64, mt), 256, 0, st>>>(
-            QeGemmArgs{S.shgu, T, nullptr, L.sh_dn, nullptr, S.sd});
+        (void)qe_launch_shared_mfma(L, S, T, false, st);
     }
     {
         QE_PROF(QP_COMBINE);
@@ -446,7 +312,7 @@ hipError_t qe_launch_layer(const QeLayerPtrs &L, const QeScratch &S, const float
 hipError_t qe_launch_dispatch(const QeScratch &S, int T, hipStream_t st) {
     const int np = T * QE_K_USED, nch = (np + 1023) / 1024;
     k_disp_hist<<<nch, 1024, 0, st>>>(S.ids, np, S.chunk_hist);
-    k_disp_scatter<<<nch, 1024, 0, st>>>(S.ids, np, S.chunk_hist, nch, QE_LARGE_TC, S.off, S.pairs, S.items,
+    k_disp_scatter<<<nch, 1024, 0, st>>>(S.ids, np, S.chunk_hist, nch, QE_MFMA_MC, S.off, S.pairs, S.items,
                                           S.n_items);
     return hipGetLastError();
 }

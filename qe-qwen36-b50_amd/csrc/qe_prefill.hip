@@ -1,0 +1,456 @@
+// Prefill expert products as MFMA grouped GEMMs (Engine::moe_round_xmx and
+// moe_xmx, engine/qe.cpp:2103-2154 and :369-436, redesigned for CDNA4).
+//
+// Exactness: the reference CPU path multiplies int8 activations by IQ4_NL
+// codebook values exactly per 32-block and applies fp32 block scales after
+// (engine/qe.cpp:704-741).  Both operands are small integers (|v| <= 127),
+// exact in fp16, so v_mfma_f32_32x32x16_f16 on them returns the exact integer
+// block dot in fp32; two MFMAs cover one 32-block.  The fp32 epilogue then
+// applies xs[m][b] * dw[n][b] per block, so results agree with the CPU path
+// to fp32 rounding.  (Scaled fp16/bf16 operands would not: the h quantisation
+// downstream turns 1e-4 relative noise into >1e-3 output error.)
+//
+// Work item: (expert e, up to 128 of its pairs in dispatch order) x N-tile.
+//   gate/up epilogue: h = silu(g)*u, quantised per 32-block (the quant_x step
+//   of engine/qe.cpp:2078-2081), stored as fp16 integers + fp32 scales;
+//   down epilogue: yp[p][n] = w_p * y.
+#include "qe_kernels.h"
+
+typedef _Float16 qe_half8 __attribute__((ext_vector_type(8)));
+typedef float qe_float16v __attribute__((ext_vector_type(16)));
+
+
+// fp16 of small integers: half(0x6400 | u) = 1024 + u for u in 0..1023, so a
+// biased byte u = v + 128 becomes v exactly after subtracting 1152.
+QE_DEV uint32_t bias_bytes_to_h2(uint32_t u4, int hi_pair) {
+    // bytes (u0,u1) or (u2,u3) of u4 -> two halves 0x64uu
+    return __builtin_amdgcn_perm(0x64646464u, u4, hi_pair ? 0x07030702u : 0x07010700u);
+}
+QE_DEV void biased4_to_half4(uint32_t u4, uint32_t &h01, uint32_t &h23) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    const h2 off = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+    uint32_t a = bias_bytes_to_h2(u4, 0), b = bias_bytes_to_h2(u4, 1);
+    h2 ha = __builtin_bit_cast(h2, a) + off, hb = __builtin_bit_cast(h2, b) + off;
+    h01 = __builtin_bit_cast(uint32_t, ha);
+    h23 = __builtin_bit_cast(uint32_t, hb);
+}
+// 8 int8 (two dwords) -> 8 fp16
+QE_DEV qe_half8 i8x8_to_half8(uint32_t lo, uint32_t hi) {
+    uint32_t h[4];
+    biased4_to_half4(lo ^ 0x80808080u, h[0], h[1]);
+    biased4_to_half4(hi ^ 0x80808080u, h[2], h[3]);
+    return __builtin_bit_cast(qe_half8, make_uint4(h[0], h[1], h[2], h[3]));
+}
+// 4 NL4 indices (one per byte) -> 4 codebook values as biased bytes (v + 128)
+QE_DEV uint32_t nl4_lookup4_biased(uint32_t idx) { return nl4_lookup4(idx) ^ 0x80808080u; }
+
+struct GemmTileArgs {
+    const uint8_t *arena;      // layer's 256 expert blobs
+    const int8_t *aq;          // int8 activations in the operand layout (qe_opnd_off), row = token or pair
+    int a_bytes;               // size of aq in bytes
+    const float *as;           // their fp32 block scales
+    int a_row_div;             // pair -> activation row: p / a_row_div (8 for tokens, 1 for pairs)
+    const int32_t *pairs;
+    const int4 *items;         // (expert, first pair, count <= 32)
+    const int32_t *n_items;
+    const float *wts;          // pair weights (down)
+    int8_t *hq; float *hs;     // gate/up output: quantised h (operand layout) + block scales
+    float *yp;                 // down output
+};
+
+// v_mfma_i32_16x16x32_i8 with one 32-element block per instruction keeps the
+// block dot an exact int32; lane l supplies k = 8 (l / 16) + 0..7 of row / column
+// l % 16 and receives D[4 (l / 16) + i][l % 16].  The 8 k of group g are the
+// block elements 4g..4g+3 and 16+4g..16+4g+3, i.e. both nibbles of code bytes
+// 4g..4g+3, so a lane's B operand is one dword of codes and its A operand one
+// 8-byte run of the operand layout.
+//
+// Wave = 64 weight rows (4 column groups of 16) x the item's <= 32 pairs (NT
+// 16-row tiles), streaming K.  Codes arrive 16 bytes per lane: lane (n, g) loads
+// block 4Q+g of its row, four 16-lane rows of the wave cover a quad of blocks,
+// and a 4x4 transpose over the rows (v_permlane32_swap, v_permlane16_swap)
+// hands lane (n, g) dword g of each block of the quad.  The load ring holds two
+// quads; loads are never predicated (the last refills wrap to the first blocks)
+// and each refill takes an offset that depends on the last read of its slot,
+// so it is issued 8 blocks ahead of its use into the slot's own registers.
+// Block scales of the wave's rows are staged once in LDS.
+//   gate/up: groups = gate j0..j0+15, j0+16..j0+31, up j0.., up j0+16.. with
+//            j0 = 32 (4 blockIdx.y + wave): h and its 32-block quantisation
+//            stay inside the wave.
+//   down:    groups = output rows 256 blockIdx.y + 64 wave + 16 c + 0..15.
+typedef unsigned qe_u32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned qe_u32x4 __attribute__((ext_vector_type(4)));
+
+// rows r of d[0..3] -> d[j] row r = d[r] row j (16-lane rows of the wave)
+QE_DEV void transpose_rows4(uint32_t d[4]) {
+    qe_u32x2 x = __builtin_amdgcn_permlane32_swap(d[0], d[2], false, false);
+    qe_u32x2 y = __builtin_amdgcn_permlane32_swap(d[1], d[3], false, false);
+    const qe_u32x2 u = __builtin_amdgcn_permlane16_swap(x.x, y.x, false, false);
+    const qe_u32x2 v = __builtin_amdgcn_permlane16_swap(x.y, y.y, false, false);
+    d[0] = u.x; d[1] = u.y; d[2] = v.x; d[3] = v.y;
+}
+
+template <bool GU> struct ExpertSmem {
+    static constexpr int NB = (GU ? QE_D : QE_FF_EXP) / 32;
+    float xs[2][NB][16];       // activation scale per (tile, block, row)
+    uint16_t dw[4][NB][16][4]; // fp16 weight scale per (wave, block, n, group)
+    int pair[32];
+};
+
+template <bool GU, int NT>
+__device__ __forceinline__ void expert_tile(const GemmTileArgs &a, const int4 it, ExpertSmem<GU> &sm) {
+    constexpr int KD = GU ? QE_D : QE_FF_EXP;  // reduction length
+    constexpr int NB = KD / 32;                // K blocks
+    constexpr int NCH = NB / 8;                // ring turns (two quads each)
+    constexpr uint32_t RB = GU ? QE_GU_ROW_BYTES : QE_DN_ROW_BYTES;
+    auto &s_xs = sm.xs;
+    auto &s_dw = sm.dw;
+    auto &s_pair = sm.pair;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, n = lane & 15, g = lane >> 4;
+    auto row_of = [&](int w, int c, int nn) {
+        return GU ? (c < 2 ? 0 : QE_FF_EXP) + (blockIdx.y * 4 + w) * 32 + 16 * (c & 1) + nn
+                  : blockIdx.y * 256 + w * 64 + 16 * c + nn;
+    };
+    const uint8_t *ebase = a.arena + (size_t)it.x * QE_EXPERT_BYTES + (GU ? 0 : QE_EXPERT_DOWN_OFF);
+    {
+        // thread = one weight row of the workgroup: its NB scales -> s_dw
+        const int c = (tid >> 4) & 3;
+        const uint4 *sc = (const uint4 *)(ebase + (size_t)row_of(wv, c, n) * RB + KD / 2);
+        uint4 v[NB / 8];
+#pragma unroll
+        for (int i = 0; i < NB / 8; ++i) v[i] = sc[i];
+#pragma unroll
+        for (int i = 0; i < NB / 8; ++i) {
+            const uint32_t w4[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+#pragma unroll
+            for (int j = 0; j < 8; ++j) s_dw[wv][8 * i + j][n][c] = (uint16_t)(w4[j >> 1] >> (16 * (j & 1)));
+        }
+    }
+    if (tid < 32) s_pair[tid] = tid < it.z ? a.pairs[it.y + tid] : -1;
+    __syncthreads();
+    {
+        float v[32 * NB / 256];
+#pragma unroll
+        for (int k = 0; k < 32 * NB / 256; ++k) {
+            const int i = tid + 256 * k, m = i / NB, b = i % NB, p = s_pair[m];
+            v[k] = p < 0 ? 0.f : a.as[(size_t)(p / a.a_row_div) * NB + b];
+        }
+#pragma unroll
+        for (int k = 0; k < 32 * NB / 256; ++k) {
+            const int i = tid + 256 * k, m = i / NB, b = i % NB;
+            s_xs[m >> 4][b][m & 15] = v[k];
+        }
+    }
+    __syncthreads();
+
+    // Buffer loads: a range-checked resource per operand (reads past the end
+    // return 0), uniform per-turn offsets in SGPRs, per-lane offsets fixed.
+    const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)ebase, (short)0, (int)(GU ? QE_EXPERT_DOWN_OFF : QE_EXPERT_BYTES - QE_EXPERT_DOWN_OFF), 0x00020000);
+    const __amdgpu_buffer_rsrc_t ar = __builtin_amdgcn_make_buffer_rsrc((void *)a.aq, (short)0, a.a_bytes, 0x00020000);
+    int rowc[4];
+    uint32_t boff[4]; // byte offset of block g of the lane's row, per column group
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        rowc[c] = row_of(wv, c, n);
+        boff[c] = (uint32_t)rowc[c] * RB + 16 * g;
+    }
+    uint32_t aoff[2];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        const int p = s_pair[16 * t + n];
+        aoff[t] = (uint32_t)((p < 0 ? s_pair[0] : p) / a.a_row_div) * KD + 16 * g; // padding rows: scale 0
+    }
+
+    float acc[4][2][4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[c][t][i] = 0.f;
+
+    // Ring: quad slot qs of turn ch holds blocks 8 ch + 4 qs .. +3; pair slot
+    // ps holds blocks 8 ch + 2 ps, +1.  Refills wrap to turn (ch + 1) % NCH.
+    uint4 rq[2][4];      // raw codes, per quad slot and column group
+    uint4 ra[4][2];      // activations, per pair slot and tile
+    auto ld128 = [](__amdgpu_buffer_rsrc_t r, uint32_t vo, int so) {
+        const qe_u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, vo, so, 0);
+        return make_uint4(v.x, v.y, v.z, v.w);
+    };
+    auto load_q = [&](int ch, int qs, uint32_t dep) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) rq[qs][c] = ld128(wr, boff[c] + dep, 128 * ch + 64 * qs);
+    };
+    auto load_a = [&](int ch, int ps, uint32_t dep) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) ra[ps][t] = ld128(ar, aoff[t] + dep, 256 * ch + 64 * ps);
+    };
+    // same issue order as the refills, so the loop's wait counts hold on entry
+    load_q(0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    load_a(0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    load_a(0, 1, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    load_q(0, 1, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    load_a(0, 2, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    load_a(0, 3, 0);
+    __builtin_amdgcn_sched_barrier(0);
+
+    for (int ch = 0; ch < NCH; ++ch) {
+        const int nx = ch + 1 < NCH ? ch + 1 : 0;
+#pragma unroll
+        for (int qs = 0; qs < 2; ++qs) {
+            uint32_t cw[4][4]; // [group][block of the quad]: the lane's code dword
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                // copy out of the ring first: the swaps overwrite their operands, and
+                // the ring registers must stay free for the refill
+                const uint32_t r4[4] = {rq[qs][c].x, rq[qs][c].y, rq[qs][c].z, rq[qs][c].w};
+#pragma unroll
+                for (int k = 0; k < 4; ++k) asm volatile("v_mov_b32 %0, %1" : "=v"(cw[c][k]) : "v"(r4[k]));
+                transpose_rows4(cw[c]);
+            }
+            {
+                uint32_t dep;
+                asm volatile("v_mov_b32 %0, 0" : "=v"(dep)
+                             : "v"(cw[0][0]), "v"(cw[1][0]), "v"(cw[2][0]), "v"(cw[3][0]));
+                load_q(nx, qs, dep);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int s = 4 * qs + j, b = 8 * ch + s, ps = s >> 1;
+                long av[2];
+#pragma unroll
+                for (int t = 0; t < NT; ++t) {
+                    const uint4 v = ra[ps][t];
+                    av[t] = (s & 1) ? (long)(((uint64_t)v.w << 32) | v.z) : (long)(((uint64_t)v.y << 32) | v.x);
+                }
+                long bv[4];
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const uint32_t q = cw[c][j];
+                    const uint32_t lo = nl4_lookup4(q & 0x0f0f0f0fu), hi = nl4_lookup4((q >> 4) & 0x0f0f0f0fu);
+                    bv[c] = (long)(((uint64_t)hi << 32) | lo);
+                }
+                typedef int i32x4 __attribute__((ext_vector_type(4)));
+                i32x4 P[2][4];
+#pragma unroll
+                for (int t = 0; t < NT; ++t)
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) {
+                        const i32x4 zero = {0, 0, 0, 0};
+                        P[t][c] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[t], bv[c], zero, 0, 0, 0);
+                    }
+                if (s & 1) {
+                    // last read of the pair slot done: refill it (see above)
+                    uint32_t dep;
+                    if (NT == 2)
+                        asm volatile("v_mov_b32 %0, 0" : "=v"(dep)
+                                     : "v"(P[0][0][0]), "v"(P[0][1][0]), "v"(P[0][2][0]), "v"(P[0][3][0]),
+                                       "v"(P[1][0][0]), "v"(P[1][1][0]), "v"(P[1][2][0]), "v"(P[1][3][0]));
+                    else
+                        asm volatile("v_mov_b32 %0, 0" : "=v"(dep)
+                                     : "v"(P[0][0][0]), "v"(P[0][1][0]), "v"(P[0][2][0]), "v"(P[0][3][0]));
+                    load_a(nx, ps, dep);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                const uint2 d2 = *(const uint2 *)&s_dw[wv][b][n][0];
+                float dw[4];
+                dw[0] = f16_bits_to_f32((uint16_t)(d2.x & 0xffffu));
+                dw[1] = f16_bits_to_f32((uint16_t)(d2.x >> 16));
+                dw[2] = f16_bits_to_f32((uint16_t)(d2.y & 0xffffu));
+                dw[3] = f16_bits_to_f32((uint16_t)(d2.y >> 16));
+#pragma unroll
+                for (int t = 0; t < NT; ++t) {
+                    const float4 x4 = *(const float4 *)&s_xs[t][b][4 * g];
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) {
+                        acc[c][t][0] = fmaf((float)P[t][c][0], x4.x * dw[c], acc[c][t][0]);
+                        acc[c][t][1] = fmaf((float)P[t][c][1], x4.y * dw[c], acc[c][t][1]);
+                        acc[c][t][2] = fmaf((float)P[t][c][2], x4.z * dw[c], acc[c][t][2]);
+                        acc[c][t][3] = fmaf((float)P[t][c][3], x4.w * dw[c], acc[c][t][3]);
+                    }
+                }
+            }
+        }
+    }
+
+    // lane holds rows 16 t + 4 g + i, column n of each group
+    if (GU) {
+        const int jb = blockIdx.y * 4 + wv; // 32-block of h
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            if (t >= NT) break;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float h0 = silu_mul(acc[0][t][i], acc[2][t][i]);
+                const float h1 = silu_mul(acc[1][t][i], acc[3][t][i]);
+                float m = fmaxf(fabsf(h0), fabsf(h1));
+#pragma unroll
+                for (int off = 1; off < 16; off <<= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+                float d;
+                const float id = quant_scale_inv(m, d);
+                const int p = s_pair[16 * t + 4 * g + i];
+                if (p >= 0) {
+                    int8_t *hrow = a.hq + (size_t)p * QE_FF_EXP + (jb >> 1) * 64 + (n >> 2) * 16 + (jb & 1) * 8 + (n & 3);
+                    hrow[0] = quant_one(h0, id);
+                    hrow[4] = quant_one(h1, id);
+                    if (n == 0) a.hs[(size_t)p * (QE_FF_EXP / 32) + jb] = d;
+                }
+            }
+        }
+    } else {
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            if (t >= NT) break;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int p = s_pair[16 * t + 4 * g + i];
+                if (p < 0) continue;
+                const float w = a.wts[p];
+                float *yrow = a.yp + (size_t)p * QE_D;
+#pragma unroll
+                for (int c = 0; c < 4; ++c) yrow[rowc[c]] = w * acc[c][t][i];
+            }
+        }
+    }
+}
+
+// One launch per GEMM; an item of <= 16 pairs runs the one-tile body.
+template <bool GU>
+__global__ __launch_bounds__(256, 2) void k_expert_mfma(GemmTileArgs a) {
+    __shared__ ExpertSmem<GU> sm;
+    if ((int)blockIdx.x >= *a.n_items) return;
+    const int4 it = a.items[blockIdx.x];
+    if (it.z > 16)
+        expert_tile<GU, 2>(a, it, sm);
+    else
+        expert_tile<GU, 1>(a, it, sm);
+}
+
+hipError_t qe_launch_expert_mfma(const QeLayerPtrs &L, const QeScratch &S, int T, hipStream_t st) {
+    const int np = T * QE_K_USED;
+    const int max_items = np / QE_MFMA_MC + QE_N_EXPERT;
+    GemmTileArgs g{};
+    g.arena = L.arena; g.pairs = S.pairs; g.items = S.items; g.n_items = S.n_items; g.wts = S.wts;
+    g.aq = S.xqp; g.a_bytes = T * QE_D; g.as = S.xs; g.a_row_div = QE_K_USED; g.hq = S.hqp; g.hs = S.hs;
+    k_expert_mfma<true><<<dim3(max_items, QE_FF_EXP / 128), 256, 0, st>>>(g);
+    g.aq = S.hqp; g.a_bytes = np * QE_FF_EXP; g.as = S.hs; g.a_row_div = 1; g.yp = S.yp;
+    k_expert_mfma<false><<<dim3(max_items, QE_D / 256), 256, 0, st>>>(g);
+    return hipGetLastError();
+}
+
+// ===========================================================================
+// Shared expert (Q8 weights, fp32 activations; engine/qe.cpp:2469, :1656,
+// :1960-1963) as MFMA GEMMs.  Q8 values are exact in fp16; an fp32
+// activation a is split into fp16 a_hi = fp16(a) and a_lo = fp16(a - a_hi), so
+// two MFMA chains into one accumulator give sum (a_hi + a_lo) w, within ~2^-22
+// of the fp32 product (activation magnitudes below 65504).  The per-block Q8
+// scale is applied in a one-fma epilogue.
+//   gate_up: A = xn [T][2048], N-tile = gate rows j0..j0+63 (waves 0,1) and up
+//            rows j0..j0+63 (waves 2,3), output h_sh[T][512] = silu(g) * u.
+//   down:    A = h_sh [T][512], N-tile = 128 down rows, output sd[T][2048].
+// Workgroup = 32 tokens x 128 columns, 32 columns per wave.
+// ===========================================================================
+QE_DEV void f32x8_to_hilo(const float4 v0, const float4 v1, qe_half8 &hi, qe_half8 &lo) {
+    const float f[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const _Float16 h = (_Float16)f[j];
+        hi[j] = h;
+        lo[j] = (_Float16)(f[j] - (float)h);
+    }
+}
+// 8 int8 (two dwords) -> 8 fp16, exact
+QE_DEV qe_half8 q8x8_to_half8(uint32_t lo, uint32_t hi) { return i8x8_to_half8(lo, hi); }
+
+template <bool GU>
+__global__ __launch_bounds__(256) void k_shared_mfma(const float *A, int T, const uint8_t *W, float *out) {
+    constexpr int KD = GU ? QE_D : QE_FF_SH;
+    constexpr int NB = KD / 32;
+    constexpr size_t RB = (size_t)KD + KD / 32 * 2;
+    __shared__ float s_up[2][16][64];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, l32 = lane & 31, kq = lane >> 5;
+    const int m0 = blockIdx.x * 32;
+    // this wave's 32 columns
+    int row;
+    if (GU) row = (wv < 2 ? 0 : QE_FF_SH) + blockIdx.y * 64 + (wv & 1) * 32 + l32;
+    else row = blockIdx.y * 128 + wv * 32 + l32;
+    const uint8_t *wrow = W + (size_t)row * RB;
+    const int m = m0 + l32;
+    const float *arow = m < T ? A + (size_t)m * KD : nullptr;
+
+    qe_float16v acc;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[i] = 0.f;
+    float4 a_nx[4];
+    uint2 w_nx[2];
+    uint16_t s_nx;
+    auto fetch = [&](int b) {
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            const int k0 = b * 32 + 16 * s + 8 * kq;
+            if (arow) {
+                a_nx[2 * s] = *(const float4 *)(arow + k0);
+                a_nx[2 * s + 1] = *(const float4 *)(arow + k0 + 4);
+            } else {
+                a_nx[2 * s] = make_float4(0.f, 0.f, 0.f, 0.f);
+                a_nx[2 * s + 1] = a_nx[2 * s];
+            }
+            w_nx[s] = *(const uint2 *)(wrow + k0);
+        }
+        s_nx = ((const uint16_t *)(wrow + KD))[b];
+    };
+    fetch(0);
+    for (int b = 0; b < NB; ++b) {
+        float4 av[4] = {a_nx[0], a_nx[1], a_nx[2], a_nx[3]};
+        const uint2 wv2[2] = {w_nx[0], w_nx[1]};
+        const float dw = f16_bits_to_f32(s_nx);
+        if (b + 1 < NB) fetch(b + 1);
+        qe_float16v p = {};
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            qe_half8 hi, lo;
+            f32x8_to_hilo(av[2 * s], av[2 * s + 1], hi, lo);
+            const qe_half8 bf = q8x8_to_half8(wv2[s].x, wv2[s].y);
+            p = __builtin_amdgcn_mfma_f32_32x32x16_f16(hi, bf, p, 0, 0, 0);
+            p = __builtin_amdgcn_mfma_f32_32x32x16_f16(lo, bf, p, 0, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[i] = fmaf(dw, p[i], acc[i]);
+    }
+    // lane holds rows m0 + 8 (i / 4) + 4 kq + (i % 4) of column `row`
+    if (GU) {
+        if (wv >= 2) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) s_up[wv - 2][i][lane] = acc[i];
+        }
+        __syncthreads();
+        if (wv < 2) {
+            const int j = blockIdx.y * 64 + wv * 32 + l32;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int mm = m0 + 8 * (i / 4) + 4 * kq + (i % 4);
+                if (mm < T) out[(size_t)mm * QE_FF_SH + j] = silu_mul(acc[i], s_up[wv][i][lane]);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int mm = m0 + 8 * (i / 4) + 4 * kq + (i % 4);
+            if (mm < T) out[(size_t)mm * QE_D + row] = acc[i];
+        }
+    }
+}
+
+hipError_t qe_launch_shared_mfma(const QeLayerPtrs &L, const QeScratch &S, int T, bool gate_up, hipStream_t st) {
+    const unsigned mt = (unsigned)((T + 31) / 32);
+    if (gate_up) k_shared_mfma<true><<<dim3(mt, QE_FF_SH / 64), 256, 0, st>>>(S.xn, T, L.sh_gu, S.shgu);
+    else k_shared_mfma<false><<<dim3(mt, QE_D / 128), 256, 0, st>>>(S.shgu, T, L.sh_dn, S.sd);
+    return hipGetLastError();
+}
