@@ -33,6 +33,7 @@ N_LAYERS = 40
 FLOP_PER_TOKEN = 8 * 6291456 + 6291456 + 2 * 257 * 2048  # 57,675,776
 HBM_PEAK = 8.0e12
 SEED = 0x51E3_6B50
+TRAFFIC_FILE = "profiles/k_decode_cfg2_pmc.txt"
 
 
 def log(msg):
@@ -50,40 +51,57 @@ def timed(torch, fn, steps, stream):
     return a.elapsed_time(b) / steps
 
 
-def cpu_baseline(n_layers_sample, tokens_sample, threads):
-    """Reference CPU MoE path (AVX2 port) on a bounded sample: tokens_sample
-    tokens, each through n_layers_sample distinct layers (B=1 decode), all on
-    host cores.  Returns tokens/s scaled to the 40-layer stack."""
+def cpu_baseline(n_distinct, budget_s, max_tokens, threads):
+    """The reference CPU MoE path (the AVX2 restatement in oracle/qe_oracle.cpp,
+    full layer: norm, router, top-8, dispatch, int8 experts, Q8 shared expert,
+    combine, residual) decoding B=1 tokens through the 40-layer stack on host
+    cores.  Bounded sample: n_distinct synthetic layers (all 256 experts each)
+    are cycled to form the 40 layer steps, and tokens run until budget_s of
+    timed CPU work (or max_tokens).  Returns (tokens/s, seconds, tokens)."""
     sys.path.insert(0, os.path.join(REPO, "oracle"))
     import oracle as O
 
-    layers = [O.SynthLayer(SEED + 7, l) for l in range(n_layers_sample)]
-    pn = np.ones(2048, np.float32)
-    xs = [O.gen_x(SEED + 7, 1000 + t, 1) for t in range(tokens_sample)]
-    # pre-generate the experts every (token, layer) will route to, outside the timing
-    plans = []
-    for t in range(tokens_sample):
-        h = xs[t]
-        for L in layers:
-            r = O.moe_layer(L, h, norm=True, residual=True)
-            plans.append(r["ids"])
-            h = r["out"]
-    ptr_sets = []
-    for L in layers:
+    layers, ptr_sets, blobs = [], [], []
+    for l in range(n_distinct):
+        L = O.SynthLayer(SEED + 7, l)
         ptrs = (ctypes.c_void_p * 256)()
+        for e in range(256):
+            b = O.gen_expert(SEED + 7, l, e)
+            blobs.append(b)
+            ptrs[e] = b.ctypes.data
+        layers.append(L)
         ptr_sets.append(ptrs)
-    for i, ids in enumerate(plans):
-        L = layers[i % n_layers_sample]
-        for e, blob in L.experts(ids).items():
-            ptr_sets[i % n_layers_sample][e] = blob.ctypes.data
-    total = 0.0
-    for t in range(tokens_sample):
-        h = xs[t]
-        for li, L in enumerate(layers):
-            sec, h = O.baseline_layer(h, pn, L, ptr_sets[li], 1, threads)
+    pn = np.ones(2048, np.float32)
+    total, tokens = 0.0, 0
+    while tokens < max_tokens and (total < budget_s or tokens == 0):
+        h = O.gen_x(SEED + 7, 1000 + tokens, 1)
+        for step in range(N_LAYERS):
+            li = step % n_distinct
+            sec, h = O.baseline_layer(h, pn, layers[li], ptr_sets[li], 1, threads)
             total += sec
-    per_layer = total / (tokens_sample * n_layers_sample)
-    return 1.0 / (per_layer * N_LAYERS), total
+        tokens += 1
+    return tokens / total, total, tokens
+
+
+def pmc_traffic(path):
+    """HBM bytes per k_decode dispatch from the committed rocprofv3 --pmc summary
+    (FETCH_SIZE and WRITE_SIZE in KiB per dispatch, each divided by the factor
+    the same counter reads for a plain copy of known size).  None if absent."""
+    if not os.path.exists(path):
+        return None
+    kv = {}
+    for line in open(path):
+        if ":" in line and not line.startswith("#"):
+            k, v = line.split(":", 1)
+            try:
+                kv[k.strip()] = float(v.split()[0])
+            except (ValueError, IndexError):
+                pass
+    try:
+        return (kv["fetch_kib_per_dispatch"] / kv["copy_fetch_factor"]
+                + kv["write_kib_per_dispatch"] / kv["copy_write_factor"]) * 1024.0
+    except KeyError:
+        return None
 
 
 def main():
@@ -94,8 +112,11 @@ def main():
     ap.add_argument("--graph", action="store_true", help="replay a captured HIP graph (one launch per step anyway)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
-    ap.add_argument("--cpu-layers", type=int, default=8)
-    ap.add_argument("--cpu-tokens", type=int, default=8)
+    ap.add_argument("--cpu-layers", type=int, default=8, help="distinct synthetic layers cycled by the CPU baseline")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="timed CPU work of the baseline sample")
+    ap.add_argument("--cpu-threads", type=int, default=16, help="host threads of the CPU baseline (the box's CPU share)")
+    ap.add_argument("--copy-bytes", type=int, default=0,
+                    help="only run a plain device copy of this many bytes 5 times (PMC calibration) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
@@ -103,10 +124,20 @@ def main():
         sys.exit(2)
 
     import torch
-    import qe_moe
 
     assert torch.cuda.is_available(), "no GPU visible"
     dev = torch.device("cuda:0")
+    if args.copy_bytes:
+        src = torch.empty(args.copy_bytes, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes": args.copy_bytes, "copies": 5}))
+        return
+
+    import qe_moe
+
     stream = torch.cuda.current_stream()
 
     # ---------------- config 2: 40-layer decode, B=1 ----------------
@@ -207,14 +238,15 @@ def main():
     # ---------------- CPU baseline ----------------
     cpu = None
     if not args.no_cpu_baseline:
-        threads = min(os.cpu_count() or 1, 16)
-        log(f"cpu baseline: {args.cpu_tokens} tokens x {args.cpu_layers} layers, {threads} threads")
-        cpu_tok_s, cpu_sec = cpu_baseline(args.cpu_layers, args.cpu_tokens, threads)
+        threads = max(1, min(os.cpu_count() or 1, args.cpu_threads))
+        log(f"cpu baseline: {args.cpu_layers} distinct layers cycled over 40 steps, ~{args.cpu_seconds} s, {threads} threads")
+        cpu_tok_s, cpu_sec, cpu_tok = cpu_baseline(args.cpu_layers, args.cpu_seconds, 100000, threads)
         cpu = {"value": round(cpu_tok_s, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
-               "sample": f"{args.cpu_tokens} tokens x {args.cpu_layers} distinct layers of the config-2 stack (B=1 decode, "
-                         f"full layer: norm, router, top-8, dispatch, int8 experts, Q8 shared, combine, residual), "
-                         f"{cpu_sec:.2f} s of CPU time, scaled to 40 layers"}
+               "sample": f"{cpu_tok} tokens of B=1 decode through the 40-step stack ({args.cpu_layers} distinct seeded "
+                         f"layers with all 256 experts each, cycled), full layer per step: norm, router, top-8, "
+                         f"dispatch, int8 experts, Q8 shared, combine, residual; {cpu_sec:.2f} s of timed CPU work"}
 
+    traffic = pmc_traffic(os.path.join(REPO, TRAFFIC_FILE))
     out = {
         "metric": METRIC, "value": round(tok_s, 2), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak",
@@ -226,7 +258,9 @@ def main():
         **pre,
         "roofline": {"kernel": "k_decode (persistent: 40 layers x norm, router, top-8, experts, shared, combine)",
                      "bound": "hbm", "achieved": round(achieved / 1e9, 2), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK, 4), "traffic": None, "bytes_per_launch": dec_bytes,
+                     "frac": round(achieved / HBM_PEAK, 4),
+                     "traffic": None if traffic is None else round(traffic), "traffic_source": TRAFFIC_FILE,
+                     "bytes_per_launch": dec_bytes,
                      "avg_us": round(dec_avg_s * 1e6, 3)},
         "kernels": kernels,
         "cpu_baseline": cpu,

@@ -20,6 +20,14 @@
 // squares use the canonical order of canon_dot() below, which the HIP kernels
 // reproduce exactly so that routing is bit-exact.
 //
+// Parity unpinned: nothing available here pins the reference's GPU kernel
+// outputs (Intel sub-group reduction order, icpx contraction, the XMX
+// accumulation of engine/qe.cpp:394-431), its oneMKL fp16 GEMM for the router
+// and shared expert at T >= 16 (engine/qe.cpp:284-294), or the ggml IQ4_NL
+// quantizer (qconv.cpp:93, off the hot path).  The checker follows the CPU
+// AVX2 path instead; tests/test_oracle_pins.py pins each function below by
+// closed forms, special cases, brute force and the routing-record fixture.
+//
 // Every function has a scalar form; quant_x and the NL4 block dot also have an
 // AVX2 form written with the same intrinsic sequence semantics as the
 // reference, and the tests require the two forms to agree bit for bit.
