@@ -4,23 +4,31 @@
 //
 // Why persistent: on MI355X every kernel launch costs ~4.5 us of fixed
 // duration (dispatch over 8 XCDs + end-of-kernel L2 write-back), while one
-// B=1 layer moves 19.6 MB = 2.5 us at 8 TB/s.  Per layer this kernel runs
-//   R  norm + router rows + shared gate|up row pairs   -> logits, silu(g)*u
-//   G  top-8 + dispatch (every workgroup, redundantly), routed gate/up +
-//      SwiGLU on 32-row units, quantised in place      -> int8 h + scales
-//   D  routed down, shared down, combine, residual      -> next x
-// Synchronisation is carried by the data: every value crossing workgroups is
-// written as one 64-bit agent-scope store {value, tag}, where the tag names
-// (launch epoch, layer, stage).  A consumer polls the entries it needs until
-// every tag matches, so one store->load round trip both synchronises and
-// delivers the data -- no barrier counters, no L2 write-back fences.  Agent
-// scope makes the compiler emit sc1 loads/stores, coherent across the XCDs'
-// separate L2s.  The dataflow orders buffer reuse: a producer can only start
-// layer l+1's stage after every workgroup has consumed layer l's data of the
-// same buffer (each stage needs contributions from every workgroup).
-// Weights a stage will need and that do not depend on the data being waited
-// for (router/shared rows, the down rows of the routed experts, the shared
-// down row) are loaded into registers before the wait.
+// B=1 layer moves 19.6 MB = 2.5 us at 8 TB/s.
+//
+// One 1024-thread workgroup (16 waves) per CU.  Per layer:
+//   R  x -> RMSNorm -> int8 x (every workgroup, redundantly); router rows and
+//      shared gate|up row pairs, one wave per row task      -> logits, silu(g)*u
+//   G  top-8 + dispatch (every workgroup, redundantly); routed gate/up + SwiGLU
+//      on units of 16 (T = 1) or 32 (T > 1) hidden rows of one expert, spread
+//      over all workgroups                                    -> h
+//   D  routed down (rows prefetched into registers during G), shared down, combine,
+//      residual, 8 output rows per workgroup                  -> next x
+// Every value crossing workgroups is one 64-bit agent-scope store {value, tag}
+// with tag = (launch epoch, layer, stage), so a reader verifies what it reads.
+// Agent-scope relaxed atomics compile to sc1 accesses, coherent across the
+// XCDs' separate L2s without write-back fences.  The logits and the shared
+// activations are polled directly; the all-gathers of x and h first wait on
+// stage counters (groups of 16 workgroups) and then read their data once.
+// Every exchanged buffer and counter exists in REP copies: producers write
+// all of them, a workgroup reads copy blockIdx % REP, so ~32 workgroups poll
+// any one cache line instead of all 256 (the shared lines otherwise queue
+// the polls at their memory channel: ~5 us per exchange against a 0.6 us
+// one-way store->load latency measured between two workgroups).
+// Buffer reuse is ordered by the data flow: a workgroup writes a stage's
+// buffer for layer l+1 only after a wait that proves every workgroup has
+// finished reading it for layer l.  Weights a stage needs that do not depend
+// on the data being waited for are loaded before the wait.
 #include "qe_kernels.h"
 
 #define LD_A(p) __hip_atomic_load((p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
@@ -28,108 +36,153 @@
 #define ADD_A(p, v) __hip_atomic_fetch_add((p), (v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
 
 #define DEC_T QE_SMALL_T
-#define DEC_PFI 16        /* items whose down rows are prefetched into LDS during G */
+#define NWV 16            /* waves per workgroup */
+#define NTH (NWV * 64)
+#define DEC_PFI 16        /* items whose down rows are prefetched into registers during G */
 #define SYNC_EPOCH 0
 #define SYNC_EXIT 32
-#define SYNC_CTR 64       /* 3 stages x 16 groups, 32 words apart: R, G, D */
+#define SYNC_CTR 64       /* per replica: 3 stages x 16 groups, 32 words apart: (unused), G, D */
+#define REP 8             /* copies of every exchanged buffer and counter */
+#define CTR_REP (3 * 16 * 32)
 #define SPIN_CAP (1 << 22)
-
-#define DEC_MIN_GRID 64   /* D rows per workgroup stay <= 32 */
+#define DEC_MIN_GRID 64   /* D row groups per workgroup stay <= 4 */
+#define N_RTASK (QE_ROUTER_ROWS + QE_FF_SH) /* router rows, then shared (gate, up) row pairs */
 
 // LDS layout (bytes)
-#define L_XQ 0                                      // int8 [T][2048]   quantised xn
-#define L_XS (L_XQ + DEC_T * QE_D)                  // f32 [T][64]      its block scales
-#define L_RES (L_XS + DEC_T * 64 * 4)               // f32 [T][32]      raw x of this workgroup's D rows
-#define L_HSH (L_RES + DEC_T * 32 * 4)              // f32 [T][512]     shared-expert silu(g)*u
-#define L_U (L_HSH + DEC_T * QE_FF_SH * 4)          // union, by stage:
-#define L_XN L_U                                    //   R: f32 [T][32][64] xn, element-interleaved
-#define L_H L_U                                     //   G: f32 [8][32] h of one 32-row unit
-#define L_HQ L_U                                    //   D: int8 [T*8][512] quantised h
+#define L_U 0                                       // union, by stage:
+#define L_XN L_U                                    //   R: f32 [T][32][64] xn, element-interleaved (raw x first)
+#define L_GU L_U                                    //   G: f32 [64 rows][8 pairs] gate/up dots of a unit
+#define L_HF L_U                                    //   D: f32 [8][512] fp32 h (T = 1)
+#define L_HQ (L_U + 8 * QE_FF_EXP * 4)              //   D: int8 [T*8][512] quantised h
 #define L_HS (L_HQ + DEC_T * 8 * QE_FF_EXP)         //   D: f32 [T*8][16] its block scales
+#define L_Y (L_HS + DEC_T * 8 * 16 * 4)             //   D: f32 [8 rows][2 halves][T] partials, [8][T] sd
 #define L_U_END (L_U + DEC_T * QE_D * 4)
-#define L_DW L_U_END                                // uint4 [4 waves][PFI][2 rows][16 blocks] down codes
-#define L_DS (L_DW + 4 * DEC_PFI * 2 * 16 * 16)     // u32   [4 waves][PFI][2 rows][16 blocks] down scales
-#define L_ITEMS (L_DS + 4 * DEC_PFI * 2 * 16 * 4)   // int4 [64]
+#define L_XQ L_U_END                                // int8 [T][2048]   quantised xn
+#define L_XS (L_XQ + DEC_T * QE_D)                  // f32 [T][64]      its block scales
+#define L_HSH (L_XS + DEC_T * 64 * 4)               // f32 [T][512]     shared-expert silu(g)*u
+#define L_RES (L_HSH + DEC_T * QE_FF_SH * 4)        // f32 [T][32]      raw x of this workgroup's D rows
+#define L_RW (L_RES + DEC_T * 32 * 4)               // [4 waves][8 KB] prefetched weights of the first row task
+#define L_ITEMS (L_RW + 4 * 8192)                   // int4 [64]
 #define L_PAIRS (L_ITEMS + 64 * 16)                 // int [64]
 #define L_IDS (L_PAIRS + 64 * 4)                    // int [64]
 #define L_WTS (L_IDS + 64 * 4)                      // f32 [64]
 #define L_SHG (L_WTS + 64 * 4)                      // f32 [8]
 #define L_MISC (L_SHG + 8 * 4)                      // int [16]
 #define L_TOTAL (L_MISC + 16 * 4)
-static_assert(L_HS + DEC_T * 8 * 16 * 4 <= L_U_END, "D-stage LDS must fit in the union");
+static_assert(L_Y + (8 * 2 * DEC_T + 8 * DEC_T) * 4 <= L_U_END, "D-stage LDS must fit in the union");
+static_assert(64 * 8 * 4 <= L_HQ - L_U, "G-stage LDS must fit in front of the D buffers");
+static_assert(L_TOTAL <= 160 * 1024, "LDS budget of one workgroup per CU");
 
 // exchange buffer offsets (u64 words, {value or payload, tag})
 #define EX_X 0                                      // 2 x [T][2048] f32
 #define EX_L (EX_X + 2 * DEC_T * QE_D)              // [T][257] f32 logits
 #define EX_HSH (EX_L + DEC_T * QE_ROUTER_ROWS)      // [T][512] f32 shared silu(g)*u
 #define EX_HQ (EX_HSH + DEC_T * QE_FF_SH)           // [T*8][16][9]: 8 x int8x4, 1 x f32 scale
-#define EX_TOTAL (EX_HQ + DEC_T * 8 * 16 * 9)
-static_assert(EX_TOTAL == QE_DECODE_EX_WORDS, "exchange size must match the allocation");
+#define EX_HF (EX_HQ + DEC_T * 8 * 16 * 9)          // [8][512] f32 h (T = 1)
+#define EX_TOTAL (EX_HF + 8 * QE_FF_EXP)           // one replica
+static_assert(REP * EX_TOTAL == QE_DECODE_EX_WORDS, "exchange size must match the allocation");
+static_assert(SYNC_CTR + REP * CTR_REP <= QE_DECODE_SYNC_WORDS, "sync words must match the allocation");
 
 QE_DEV uint64_t pack_tv(float v, unsigned tag) { return ((uint64_t)tag << 32) | __float_as_uint(v); }
 QE_DEV float tv_val(uint64_t w) { return __uint_as_float((unsigned)w); }
-QE_DEV bool tv_ok(uint64_t w, unsigned tag) { return (unsigned)(w >> 32) == tag; }
 
-// Wave-uniform poll of N tagged entries per lane at src[i * stride]: reload
-// until every lane sees `tag` on all of them (bounded; a timeout sets *err).
+// Read N tagged words w[i] = src[i * stride] until every one carries `tag`
+// (wave-uniform retry, bounded; a timeout sets *err).  Inactive lanes read nothing.
 template <int N>
-QE_DEV void poll_tv(const uint64_t *src, int stride, unsigned tag, float out[N], unsigned *err) {
-    uint64_t w[N];
+QE_DEV void read_tv(const uint64_t *src, int stride, unsigned tag, uint64_t w[N], bool act, unsigned *err) {
     for (int spins = 0;; ++spins) {
-#pragma unroll
-        for (int i = 0; i < N; ++i) w[i] = LD_A((uint64_t *)src + (size_t)i * stride);
         unsigned bad = 0;
 #pragma unroll
-        for (int i = 0; i < N; ++i) bad |= (unsigned)(w[i] >> 32) ^ tag;
+        for (int i = 0; i < N; ++i) {
+            w[i] = act ? LD_A((uint64_t *)src + (size_t)i * stride) : ((uint64_t)tag << 32);
+            bad |= (unsigned)(w[i] >> 32) ^ tag;
+        }
         if (__all(bad == 0)) break;
         if (spins > SPIN_CAP) { ST_A(err, 1u); break; }
         __builtin_amdgcn_s_sleep(1);
     }
+}
+
+// As read_tv, with two reads of the N words in flight (polls of small data
+// that is usually not there yet: logits, shared activations).
+template <int N>
+QE_DEV void poll_tv2(const uint64_t *src, int stride, unsigned tag, uint64_t w[N], bool act, unsigned *err) {
+    uint64_t b[2][N];
+    auto issue = [&](uint64_t *d) {
 #pragma unroll
-    for (int i = 0; i < N; ++i) out[i] = tv_val(w[i]);
+        for (int i = 0; i < N; ++i) d[i] = act ? LD_A((uint64_t *)src + (size_t)i * stride) : ((uint64_t)tag << 32);
+    };
+    auto ok = [&](const uint64_t *d) {
+        unsigned bad = 0;
+#pragma unroll
+        for (int i = 0; i < N; ++i) bad |= (unsigned)(d[i] >> 32) ^ tag;
+        return __all(bad == 0);
+    };
+    issue(b[0]);
+    __builtin_amdgcn_s_sleep(4);
+    issue(b[1]);
+    for (int spins = 0;; spins += 2) {
+        if (ok(b[0])) {
+#pragma unroll
+            for (int i = 0; i < N; ++i) w[i] = b[0][i];
+            return;
+        }
+        issue(b[0]);
+        __builtin_amdgcn_s_sleep(4);
+        if (ok(b[1])) {
+#pragma unroll
+            for (int i = 0; i < N; ++i) w[i] = b[1][i];
+            return;
+        }
+        issue(b[1]);
+        __builtin_amdgcn_s_sleep(4);
+        if (spins > SPIN_CAP) {
+            ST_A(err, 1u);
+#pragma unroll
+            for (int i = 0; i < N; ++i) w[i] = b[1][i];
+            return;
+        }
+    }
 }
 
 // Stage counters: after issuing all of its tagged data stores a workgroup
 // bumps its group's counter for the stage (groups of 16 workgroups; the add
 // is posted, nothing waits on it).  A consumer's wave 0 polls the <= 16 group
-// counters of the stage until each reaches 16 * (layer + 1), then every
-// thread reads its data once (tags verified, rare retry).  Measured on
-// MI355X with 256 workgroups: ~4.2 us per all-gather this way, against
-// ~5.5 us polling one flag per workgroup and ~5.7 us polling the data itself.
-QE_DEV void stage_arrive(unsigned *ctr) {
+// counters of the stage until each reaches 16 * round, then every thread
+// reads its data once (tags verified, rare retry).  Measured on MI355X with
+// 256 workgroups: ~4.2 us per all-gather this way, against ~5.5 us polling
+// one flag per workgroup and ~5.7 us polling the data itself.
+QE_DEV void stage_arrive(unsigned *ctr) { // ctr: replica 0 of the stage
     __syncthreads();
-    if (threadIdx.x == 0) (void)ADD_A(ctr + (blockIdx.x >> 4) * 32, 1u);
+    if (threadIdx.x < REP) (void)ADD_A(ctr + threadIdx.x * CTR_REP + (blockIdx.x >> 4) * 32, 1u);
 }
+// The poll keeps four loads in flight, spaced by a short sleep, so a count
+// that lands is seen ~1/4 of a memory round trip later rather than up to one.
 QE_DEV void stage_wait(const unsigned *ctr, unsigned round, unsigned *err) {
     if (threadIdx.x < 64) {
         const int g = threadIdx.x, ng = (gridDim.x + 15) >> 4;
         const unsigned gsz = (unsigned)((g + 1) * 16 <= (int)gridDim.x ? 16 : (int)gridDim.x - g * 16);
-        for (int spins = 0;; ++spins) {
-            const bool ok = g >= ng || LD_A((unsigned *)ctr + g * 32) >= gsz * round;
-            if (__all(ok)) break;
+        const unsigned want = g < ng ? gsz * round : 0u;
+        unsigned *p = (unsigned *)ctr + (blockIdx.x % REP) * CTR_REP + (g < ng ? g : 0) * 32;
+        unsigned v[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            v[i] = LD_A(p);
+            __builtin_amdgcn_s_sleep(2);
+        }
+        for (int spins = 0;; spins += 4) {
+            bool done = false;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                if (__all(v[i] >= want)) { done = true; break; }
+                v[i] = LD_A(p);
+                __builtin_amdgcn_s_sleep(2);
+            }
+            if (done) break;
             if (spins > SPIN_CAP) { ST_A(err, 1u); break; }
-            __builtin_amdgcn_s_sleep(1);
         }
     }
     __syncthreads();
-}
-
-// Poll the 257 logits of one token in one round: v[j] = logit(lane + 64 j), v[4] = logit 256.
-QE_DEV void poll_logits(const uint64_t *row, unsigned tag, float v[5], unsigned *err) {
-    uint64_t w[5];
-    for (int spins = 0;; ++spins) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) w[j] = LD_A((uint64_t *)row + threadIdx.x % 64 + 64 * j);
-        w[4] = LD_A((uint64_t *)row + QE_N_EXPERT);
-        unsigned bad = 0;
-#pragma unroll
-        for (int j = 0; j < 5; ++j) bad |= (unsigned)(w[j] >> 32) ^ tag;
-        if (__all(bad == 0)) break;
-        if (spins > SPIN_CAP) { ST_A(err, 1u); break; }
-        __builtin_amdgcn_s_sleep(1);
-    }
-#pragma unroll
-    for (int j = 0; j < 5; ++j) v[j] = tv_val(w[j]);
 }
 
 // Order-preserving u32 image of a float (-0 folded onto +0 by the caller).
@@ -183,16 +236,59 @@ QE_DEV void wave_topk8(float v[4], float lg_sh, int lane, int *ids, float *wts, 
     }
 }
 
-__global__ __launch_bounds__(256) void k_decode(QeDecodeArgs a) {
+// Gate/up rows of one unit: this lane's NB blocks of its row (blocks c + LPR i,
+// LPR = 64 / NB lanes per row), dotted with the int8 x of every pair of the item;
+// the row total lands in s_gu[row_in_unit * 8 + pair].
+// after_loads() runs once the row's loads are issued (other loads can queue
+// behind them there without delaying this row).
+template <int NB, typename F>
+QE_DEV void unit_rows(const uint8_t *row, int c, int row_in_unit, const int4 it, const int *s_pairs,
+                      const int8_t *s_xq, const float *s_xs, float *s_gu, F &&after_loads) {
+    constexpr int LPR = 64 / NB;
+    uint4 q[NB];
+    uint16_t dwr[NB];
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+        const int b = c + LPR * i;
+        q[i] = *(const uint4 *)(row + b * 16);
+        dwr[i] = ((const uint16_t *)(row + QE_D / 2))[b];
+    }
+    after_loads();
+    float dw[NB];
+#pragma unroll
+    for (int i = 0; i < NB; ++i) dw[i] = f16_bits_to_f32(dwr[i]);
+    for (int jp = 0; jp < it.z; ++jp) {
+        const int t = s_pairs[it.y + jp] / QE_K_USED;
+        const int8_t *xq = s_xq + t * QE_D;
+        const float *xs = s_xs + t * 64;
+        float acc = 0.f;
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            const int b = c + LPR * i;
+            const nl4_blk w = nl4_decode_block(q[i]); // decoded per pair: few registers, T > 1 only repeats
+            const uint4 x0 = *(const uint4 *)(xq + b * 32), x1 = *(const uint4 *)(xq + b * 32 + 16);
+            acc = fmaf(dw[i] * xs[b], (float)nl4_block_dot(w, x0, x1), acc);
+        }
+#pragma unroll
+        for (int off = 1; off < LPR; off <<= 1) acc = acc + __shfl_xor(acc, off, 64);
+        if (c == 0) s_gu[row_in_unit * 8 + jp] = acc;
+    }
+}
+
+// TM = 1: the single-token kernel (B = 1 decode); TM = 8: any T <= 8.
+template <int TM>
+__global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
     extern __shared__ __align__(16) uint8_t lds[];
-    int8_t *s_xq = (int8_t *)(lds + L_XQ);
-    float *s_xs = (float *)(lds + L_XS);
-    float *s_res = (float *)(lds + L_RES);
-    float *s_hsh = (float *)(lds + L_HSH);
     float *s_xn = (float *)(lds + L_XN);
-    float *s_h = (float *)(lds + L_H);
+    float *s_gu = (float *)(lds + L_GU);
+    float *s_hf = (float *)(lds + L_HF);
     int8_t *s_hq = (int8_t *)(lds + L_HQ);
     float *s_hs = (float *)(lds + L_HS);
+    float *s_y = (float *)(lds + L_Y);
+    int8_t *s_xq = (int8_t *)(lds + L_XQ);
+    float *s_xs = (float *)(lds + L_XS);
+    float *s_hsh = (float *)(lds + L_HSH);
+    float *s_res = (float *)(lds + L_RES);
     int4 *s_items = (int4 *)(lds + L_ITEMS);
     int *s_pairs = (int *)(lds + L_PAIRS);
     int *s_ids = (int *)(lds + L_IDS);
@@ -200,25 +296,32 @@ __global__ __launch_bounds__(256) void k_decode(QeDecodeArgs a) {
     float *s_shg = (float *)(lds + L_SHG);
     int *s_misc = (int *)(lds + L_MISC);
 
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, l16 = lane & 15;
-    const int T = a.T, np = T * QE_K_USED;
-    const int nwaves = gridDim.x * 4, gw = blockIdx.x * 4 + wv;
-    const int n_rtask = QE_ROUTER_ROWS + QE_FF_SH; // router rows, then shared (gate, up) row pairs
+    const int T = TM == 1 ? 1 : a.T, np = T * QE_K_USED;
     const int d_iters = (QE_D / 8 + gridDim.x - 1) / gridDim.x; // D row groups of 8 per workgroup
-    if (tid == 0) s_misc[1] = (int)LD_A(a.sync + SYNC_EPOCH);
+    if (threadIdx.x == 0) s_misc[1] = (int)LD_A(a.sync + SYNC_EPOCH);
     __syncthreads();
     const unsigned epoch = (unsigned)s_misc[1];
-    uint64_t *EX = a.ex;
-    unsigned *CR = a.sync + SYNC_CTR, *CG = CR + 16 * 32, *CD = CG + 16 * 32;
+    uint64_t *EX = a.ex;                                   // replica 0 (writes go to all REP)
+    const uint64_t *EXr = a.ex + (size_t)(blockIdx.x % REP) * EX_TOTAL; // the copy this workgroup reads
+    unsigned *CG = a.sync + SYNC_CTR + 16 * 32, *CD = CG + 16 * 32;
+    constexpr bool mode16 = TM == 1; // 16-row units, fp32 h (one token: 8 items x 32 units fill the grid)
+    const int rb0 = blockIdx.x * 8;
 
     for (int li = 0; li < a.n_layers; ++li) {
+        // Thread indices re-derived per layer through an opaque copy: addresses built
+        // from them stay inside the loop instead of being hoisted out and spilled.
+        int tid = threadIdx.x;
+        asm volatile("" : "+v"(tid));
+        const int lane = tid & 63, wv = tid >> 6, l16 = lane & 15;
+        // D: wave = (row rr of the group of 8, half); items u = half + 2 s, slot s = 4 k + isub
+        const int rr = wv >> 1, half = wv & 1, isub = lane >> 4;
         const int l = a.first_layer + li;
         const bool last = li == a.n_layers - 1;
         const unsigned tagR = epoch * 65536u + (unsigned)li * 4u + 1u; // logits, shared h
-        const unsigned tagG = tagR + 1u;                               // routed int8 h
+        const unsigned tagG = tagR + 1u;                               // routed h
         const unsigned tagD = tagR + 2u;                               // x of the next layer
         const unsigned tagIn = tagR - 2u;                              // x of this layer (li > 0)
-        const uint64_t *src_x = EX + EX_X + (size_t)((li - 1) & 1) * DEC_T * QE_D;
+        const uint64_t *src_x = EXr + EX_X + (size_t)((li - 1) & 1) * DEC_T * QE_D;
         uint64_t *dst_x = EX + EX_X + (size_t)(li & 1) * DEC_T * QE_D;
         const uint8_t *arena = a.arena + (size_t)l * QE_LAYER_EXPERT_BYTES;
         const float *router = a.router + (size_t)l * QE_ROUTER_ROWS * QE_D;
@@ -227,43 +330,60 @@ __global__ __launch_bounds__(256) void k_decode(QeDecodeArgs a) {
         const uint8_t *sh_dn = a.sh_dn + (size_t)l * QE_SH_DN_BYTES;
         const float *pnorm = a.norm ? a.post_norm + (size_t)l * QE_D : nullptr;
 
-        // ================= R: router rows + shared (gate, up) pairs =================
-        // first task's weights into registers before waiting for x
-        const int task0 = gw;
-        float wr[32];
-        uint4 g0 = make_uint4(0, 0, 0, 0), g1 = g0, u0 = g0, u1 = g0;
-        float gsc = 0.f, usc = 0.f;
-        auto load_task = [&](int task) {
-            if (task < QE_ROUTER_ROWS) {
-                load32(router + (size_t)task * QE_D + lane * 32, wr);
-            } else if (task < n_rtask) {
-                const int j = task - QE_ROUTER_ROWS;
-                const uint8_t *rg = sh_gu + (size_t)j * QE_SH_GU_ROW_BYTES, *ru = sh_gu + (size_t)(QE_FF_SH + j) * QE_SH_GU_ROW_BYTES;
-                g0 = ((const uint4 *)(rg + lane * 32))[0];
-                g1 = ((const uint4 *)(rg + lane * 32))[1];
-                gsc = f16_bits_to_f32(((const uint16_t *)(rg + QE_D))[lane]);
-                u0 = ((const uint4 *)(ru + lane * 32))[0];
-                u1 = ((const uint4 *)(ru + lane * 32))[1];
-                usc = f16_bits_to_f32(((const uint16_t *)(ru + QE_D))[lane]);
-            }
-        };
-        load_task(task0);
-        if (li > 0) stage_wait(CD, (unsigned)li, a.err);
-        for (int t = wv; t < T; t += 4) {
-            float v[32];
-            if (li == 0) load32(a.x_in + (size_t)t * QE_D + lane * 32, v);
-            else poll_tv<32>(src_x + (size_t)t * QE_D + lane * 32, 1, tagIn, v, a.err);
-            if (a.residual) { // raw x of this workgroup's D rows, 8 per group, all inside one 32-chunk
-                for (int m = 0; m < d_iters; ++m) {
-                    const int rb = (blockIdx.x + m * gridDim.x) * 8;
-                    if (rb < QE_D && (rb >> 5) == lane) {
-                        const int o = rb & 31;
+        // ================= R: x, norm, router rows + shared (gate, up) pairs =================
+        // this wave's first row task into registers before waiting for x
+        // The first row task of waves 0..3 is copied into LDS before waiting for x
+        // (global->LDS, no registers held): a router row as 2048 fp32, or a shared
+        // (gate, up) pair as 2 x 2048 int8 + 2 x 64 scales, one u16 per dword.
+        const int task0 = blockIdx.x + (int)gridDim.x * wv;
+        uint8_t *rw_lds = lds + L_RW + (wv & 3) * 8192;
+        const bool rw_pref = wv < 4 && task0 < N_RTASK;
+        if (rw_pref) {
+            auto dma16 = [&](const uint8_t *src, uint8_t *dst) { // 64 lanes x 16 B, lane i -> dst + 16 i
+                __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)(src + lane * 16),
+                                                 (__attribute__((address_space(3))) void *)dst, 16, 0, 0);
+            };
+            if (task0 < QE_ROUTER_ROWS) {
+                const uint8_t *row = (const uint8_t *)(router + (size_t)task0 * QE_D);
 #pragma unroll
-                        for (int i = 0; i < 8; ++i)
-                            s_res[t * 32 + m * 8 + i] = o == 0 ? v[i] : o == 8 ? v[8 + i] : o == 16 ? v[16 + i] : v[24 + i];
-                    }
+                for (int k = 0; k < 8; ++k) dma16(row + k * 1024, rw_lds + k * 1024);
+            } else {
+                const int j = task0 - QE_ROUTER_ROWS;
+                const uint8_t *rg = sh_gu + (size_t)j * QE_SH_GU_ROW_BYTES, *ru = sh_gu + (size_t)(QE_FF_SH + j) * QE_SH_GU_ROW_BYTES;
+#pragma unroll
+                for (int k = 0; k < 2; ++k) {
+                    dma16(rg + k * 1024, rw_lds + k * 1024);
+                    dma16(ru + k * 1024, rw_lds + 2048 + k * 1024);
                 }
+                __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)(rg + QE_D + lane * 2),
+                                                 (__attribute__((address_space(3))) void *)(rw_lds + 4096), 2, 0, 0);
+                __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)(ru + QE_D + lane * 2),
+                                                 (__attribute__((address_space(3))) void *)(rw_lds + 4096 + 256), 2, 0, 0);
             }
+        }
+        if (li > 0) stage_wait(CD, (unsigned)li, a.err);
+        // raw x of all tokens -> LDS (natural layout, token stride 2048; T*2048 is a multiple of 2 NTH)
+        if (li == 0) {
+            for (int i = tid; i < T * QE_D; i += NTH) s_xn[i] = a.x_in[i];
+        } else {
+            for (int i0 = 0; i0 < T * QE_D; i0 += 2 * NTH) {
+                uint64_t w[2];
+                read_tv<2>(src_x + i0 + tid, NTH, tagIn, w, true, a.err);
+                s_xn[i0 + tid] = tv_val(w[0]);
+                s_xn[i0 + tid + NTH] = tv_val(w[1]);
+            }
+        }
+        __syncthreads();
+        if (a.residual && tid < T * 8 * d_iters) { // raw x of this workgroup's D rows
+            const int t = tid / (8 * d_iters), k = tid % (8 * d_iters), m = k >> 3;
+            const int r = (blockIdx.x + m * gridDim.x) * 8 + (k & 7);
+            s_res[t * 32 + k] = r < QE_D ? s_xn[t * QE_D + r] : 0.f;
+        }
+        if (wv < T) { // wave t: norm + quantise token t; lane = 32-element chunk (reads precede writes in LDS order)
+            const int t = wv;
+            float v[32];
+#pragma unroll
+            for (int i = 0; i < 32; ++i) v[i] = s_xn[t * QE_D + lane * 32 + i];
             wave_norm_chunk(v, pnorm, lane);
 #pragma unroll
             for (int i = 0; i < 32; ++i) s_xn[t * QE_D + i * 64 + lane] = v[i];
@@ -274,20 +394,45 @@ __global__ __launch_bounds__(256) void k_decode(QeDecodeArgs a) {
             }
         }
         __syncthreads();
-        for (int task = task0; task < n_rtask; task += nwaves) {
-            if (task != task0) load_task(task);
+        for (int task = task0; task < N_RTASK; task += (int)gridDim.x * NWV) {
+            const bool in_lds = rw_pref && task == task0;
             if (task < QE_ROUTER_ROWS) {
                 const bool add_bias = bias && task < QE_N_EXPERT;
                 const float b = add_bias ? bias[task] : 0.f;
+                float wr[32];
+                if (in_lds) {
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) *(float4 *)(wr + 4 * i) = *(const float4 *)(rw_lds + lane * 128 + 16 * i);
+                } else {
+                    load32(router + (size_t)task * QE_D + lane * 32, wr);
+                }
                 for (int t = 0; t < T; ++t) {
                     float acc = 0.f;
 #pragma unroll
                     for (int i = 0; i < 32; ++i) acc = fmaf(wr[i], s_xn[t * QE_D + i * 64 + lane], acc);
                     acc = wave_sum_canon(acc);
-                    if (lane == 0) ST_A(EX + EX_L + t * QE_ROUTER_ROWS + task, pack_tv(add_bias ? acc + b : acc, tagR));
+                    if (lane < REP) ST_A(EX + lane * EX_TOTAL + EX_L + t * QE_ROUTER_ROWS + task, pack_tv(add_bias ? acc + b : acc, tagR));
                 }
             } else {
                 const int j = task - QE_ROUTER_ROWS;
+                uint4 g0, g1, u0, u1;
+                float gsc, usc;
+                if (in_lds) {
+                    g0 = *(const uint4 *)(rw_lds + lane * 32);
+                    g1 = *(const uint4 *)(rw_lds + lane * 32 + 16);
+                    u0 = *(const uint4 *)(rw_lds + 2048 + lane * 32);
+                    u1 = *(const uint4 *)(rw_lds + 2048 + lane * 32 + 16);
+                    gsc = f16_bits_to_f32((uint16_t)*(const unsigned *)(rw_lds + 4096 + lane * 4));
+                    usc = f16_bits_to_f32((uint16_t)*(const unsigned *)(rw_lds + 4096 + 256 + lane * 4));
+                } else {
+                    const uint8_t *rg = sh_gu + (size_t)j * QE_SH_GU_ROW_BYTES, *ru = sh_gu + (size_t)(QE_FF_SH + j) * QE_SH_GU_ROW_BYTES;
+                    g0 = ((const uint4 *)(rg + lane * 32))[0];
+                    g1 = ((const uint4 *)(rg + lane * 32))[1];
+                    gsc = f16_bits_to_f32(((const uint16_t *)(rg + QE_D))[lane]);
+                    u0 = ((const uint4 *)(ru + lane * 32))[0];
+                    u1 = ((const uint4 *)(ru + lane * 32))[1];
+                    usc = f16_bits_to_f32(((const uint16_t *)(ru + QE_D))[lane]);
+                }
                 float wg[32], wu[32];
                 unpack_i8x32(g0, g1, wg);
                 unpack_i8x32(u0, u1, wu);
@@ -301,29 +446,27 @@ __global__ __launch_bounds__(256) void k_decode(QeDecodeArgs a) {
                     }
                     ag = wave_sum_canon(ag * gsc);
                     au = wave_sum_canon(au * usc);
-                    if (lane == 0) ST_A(EX + EX_HSH + t * QE_FF_SH + j, pack_tv(silu_mul(ag, au), tagR));
+                    const float hv = silu_mul(ag, au);
+                    if (lane < REP) ST_A(EX + lane * EX_TOTAL + EX_HSH + t * QE_FF_SH + j, pack_tv(hv, tagR));
                 }
             }
         }
-        stage_arrive(CR);
 
         // ================= G: top-8, dispatch, routed gate/up =================
-        stage_wait(CR, (unsigned)li + 1u, a.err);
-        for (int t = wv; t < T; t += 4) {
+        if (wv < T) {
+            const int t = wv;
+            uint64_t w[5];
+            poll_tv2<4>(EXr + EX_L + t * QE_ROUTER_ROWS + lane, 64, tagR, w, true, a.err);
+            poll_tv2<1>(EXr + EX_L + t * QE_ROUTER_ROWS + QE_N_EXPERT, 0, tagR, w + 4, true, a.err);
             float v[5];
-            poll_logits(EX + EX_L + t * QE_ROUTER_ROWS, tagR, v, a.err);
+#pragma unroll
+            for (int j = 0; j < 5; ++j) v[j] = tv_val(w[j]);
             if (last && blockIdx.x == 0) {
 #pragma unroll
                 for (int j = 0; j < 4; ++j) a.logits[t * QE_ROUTER_ROWS + lane + 64 * j] = v[j];
                 if (lane == 0) a.logits[t * QE_ROUTER_ROWS + QE_N_EXPERT] = v[4];
             }
             wave_topk8(v, v[4], lane, s_ids + t * QE_K_USED, s_wts + t * QE_K_USED, s_shg + t);
-        }
-        for (int t = 0; t < T; ++t) { // shared-expert activations of token t, used in D
-            float hv[2];
-            poll_tv<2>(EX + EX_HSH + t * QE_FF_SH + tid, 256, tagR, hv, a.err);
-            s_hsh[t * QE_FF_SH + tid] = hv[0];
-            s_hsh[t * QE_FF_SH + 256 + tid] = hv[1];
         }
         __syncthreads();
         if (wv == 0) {
@@ -364,138 +507,140 @@ __global__ __launch_bounds__(256) void k_decode(QeDecodeArgs a) {
         __syncthreads();
         const int nitems = s_misc[0];
 
-        // down rows of this workgroup's first D group (2 per wave) for the first DEC_PFI items:
-        // asynchronous global->LDS copies issued now, consumed after the G stage
-        const int rd0 = blockIdx.x * 8 + wv * 2;
-        const int pf_items = nitems < DEC_PFI ? nitems : DEC_PFI;
-        uint4 *s_dw = (uint4 *)(lds + L_DW) + wv * DEC_PFI * 32;
-        // a sub-dword global->LDS load stores each lane's value zero-extended into its own dword
-        unsigned *s_ds = (unsigned *)(lds + L_DS) + wv * DEC_PFI * 32;
-        for (int u0 = 0; u0 < pf_items; u0 += 2) {
-            const int sub = lane >> 5, u = u0 + sub < pf_items ? u0 + sub : u0; // lane -> (item, row, block)
-            const uint8_t *drow = arena + (size_t)s_items[u].x * QE_EXPERT_BYTES + QE_EXPERT_DOWN_OFF +
-                                  (size_t)(rd0 + ((lane >> 4) & 1)) * QE_DN_ROW_BYTES;
-            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)(drow + l16 * 16),
-                                             (__attribute__((address_space(3))) void *)(s_dw + u0 * 32), 16, 0, 0);
-            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)(drow + QE_FF_EXP / 2 + l16 * 2),
-                                             (__attribute__((address_space(3))) void *)(s_ds + u0 * 32), 2, 0, 0);
-        }
-        const int half = (lane >> 4) & 1, rsel = lane >> 5;
-        uint4 dq0 = make_uint4(0, 0, 0, 0), dq1 = dq0; // shared down row of the first D group
+        // Down rows of this workgroup's first D row group for the first DEC_PFI
+        // items and the wave's shared down row, loaded into registers during G
+        // (after the first unit's own loads, so the unit does not wait for them).
+        // Wave (row rr, half), round k: lane (isub, block) takes item half + 2 (4 k + isub).
+        uint4 dpq[2] = {make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0)};
+        unsigned dps[2] = {0u, 0u};
+        uint4 dq0 = make_uint4(0, 0, 0, 0), dq1 = dq0;
         uint16_t dsc = 0;
-        {
-            const uint8_t *srow = sh_dn + (size_t)(rd0 + rsel) * QE_SH_DN_ROW_BYTES;
-            dq0 = ((const uint4 *)(srow + l16 * 32))[0];
-            dq1 = ((const uint4 *)(srow + l16 * 32))[1];
-            dsc = ((const uint16_t *)(srow + QE_FF_SH))[l16];
-        }
-
-        // units: (item, 32-row block); wave w takes 8 rows, 8 lanes per row, lane owns blocks lb + 8 j
-        const int lb = lane & 7, rl = wv * 8 + (lane >> 3);
-        for (int unit = blockIdx.x; unit < nitems * 16; unit += gridDim.x) {
-            const int4 it = s_items[unit >> 4];
-            const int blk32 = unit & 15, r = blk32 * 32 + rl;
-            const uint8_t *base = arena + (size_t)it.x * QE_EXPERT_BYTES;
-            const uint8_t *rg = base + (size_t)r * QE_GU_ROW_BYTES, *ru = base + (size_t)(QE_FF_EXP + r) * QE_GU_ROW_BYTES;
-            nl4_blk dg[8], du[8];
-            float sg[8], su[8];
-            {
-                uint4 qg[8], qu[8];
-                uint16_t sgr[8], sur[8];
+        bool d_prefetched = false;
+        auto d_prefetch = [&]() {
+            if (d_prefetched) return;
+            d_prefetched = true;
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const int b = lb + 8 * j;
-                    qg[j] = *(const uint4 *)(rg + b * 16);
-                    qu[j] = *(const uint4 *)(ru + b * 16);
-                    sgr[j] = ((const uint16_t *)(rg + QE_D / 2))[b];
-                    sur[j] = ((const uint16_t *)(ru + QE_D / 2))[b];
-                }
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    dg[j] = nl4_decode_block(qg[j]);
-                    du[j] = nl4_decode_block(qu[j]);
-                    sg[j] = f16_bits_to_f32(sgr[j]);
-                    su[j] = f16_bits_to_f32(sur[j]);
+            for (int k = 0; k < 2; ++k) {
+                if (half + 8 * k < nitems) {
+                    int u = half + 2 * (4 * k + isub);
+                    if (u >= nitems) u = half + 8 * k; // a valid item; the slot is never used
+                    const uint8_t *drow = arena + (size_t)s_items[u].x * QE_EXPERT_BYTES + QE_EXPERT_DOWN_OFF +
+                                          (size_t)(rb0 + rr) * QE_DN_ROW_BYTES;
+                    dpq[k] = *(const uint4 *)(drow + l16 * 16);
+                    dps[k] = ((const uint16_t *)(drow + QE_FF_EXP / 2))[l16];
                 }
             }
-            for (int jp = 0; jp < it.z; ++jp) {
-                const int t = s_pairs[it.y + jp] / QE_K_USED;
-                float G = 0.f, U = 0.f;
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const int b = lb + 8 * j;
-                    const uint4 x0 = *(const uint4 *)(s_xq + t * QE_D + b * 32), x1 = *(const uint4 *)(s_xq + t * QE_D + b * 32 + 16);
-                    const float xsv = s_xs[t * 64 + b];
-                    G = fmaf(sg[j] * xsv, (float)nl4_block_dot(dg[j], x0, x1), G);
-                    U = fmaf(su[j] * xsv, (float)nl4_block_dot(du[j], x0, x1), U);
-                }
-#pragma unroll
-                for (int off = 1; off < 8; off <<= 1) {
-                    G = G + __shfl_xor(G, off, 64);
-                    U = U + __shfl_xor(U, off, 64);
-                }
-                if (lb == 0) s_h[jp * 32 + rl] = silu_mul(G, U);
+            if (half == 0) {
+                const uint8_t *srow = sh_dn + (size_t)(rb0 + rr) * QE_SH_DN_ROW_BYTES;
+                dq0 = ((const uint4 *)(srow + l16 * 32))[0];
+                dq1 = ((const uint4 *)(srow + l16 * 32))[1];
+                dsc = ((const uint16_t *)(srow + QE_FF_SH))[l16];
+            }
+        };
+
+        // Units of one expert item: JU hidden rows j (gate rows j, up rows 512 + j).
+        //   mode16 (T = 1): JU = 16, 32 rows; wave w < 8 -> gate rows 2w, 2w+1, w >= 8 -> up;
+        //                   32 lanes per row, a lane holds blocks c, c + 32.  h published fp32.
+        //   else:           JU = 32, 64 rows; wave w -> 4 rows, 16 lanes per row, a lane
+        //                   holds blocks c + 16 i.  h quantised per 32 rows, published int8.
+        const int JU = mode16 ? 16 : 32, upi = QE_FF_EXP / JU, nunits = nitems * upi;
+        for (int unit = blockIdx.x; unit < nunits; unit += gridDim.x) {
+            const int4 it = s_items[unit / upi];
+            const int j0 = (unit % upi) * JU;
+            const bool up = wv >= 8;
+            const uint8_t *base = arena + (size_t)it.x * QE_EXPERT_BYTES + (size_t)(up ? QE_FF_EXP : 0) * QE_GU_ROW_BYTES;
+            if (mode16) {
+                const int rw = (wv & 7) * 2 + (lane >> 5);
+                unit_rows<2>(base + (size_t)(j0 + rw) * QE_GU_ROW_BYTES, lane & 31, (up ? JU : 0) + rw, it, s_pairs,
+                             s_xq, s_xs, s_gu, d_prefetch);
+            } else {
+                const int rw = (wv & 7) * 4 + (lane >> 4);
+                unit_rows<4>(base + (size_t)(j0 + rw) * QE_GU_ROW_BYTES, l16, (up ? JU : 0) + rw, it, s_pairs,
+                             s_xq, s_xs, s_gu, d_prefetch);
             }
             __syncthreads();
-            { // quantise the unit's 32-row block of every pair: thread (pair jp, row rr)
-                const int jp = tid >> 5, rr = tid & 31;
-                const bool act = jp < it.z;
-                const float hv = act ? s_h[jp * 32 + rr] : 0.f;
+            if (mode16) {
+                if (tid < JU * it.z) { // thread (pair jp, row j)
+                    const int jp = tid / JU, j = tid % JU;
+                    const float h = silu_mul(s_gu[j * 8 + jp], s_gu[(JU + j) * 8 + jp]);
+                    const int p = s_pairs[it.y + jp];
+#pragma unroll
+                    for (int r = 0; r < REP; ++r) ST_A(EX + r * EX_TOTAL + EX_HF + (size_t)p * QE_FF_EXP + j0 + j, pack_tv(h, tagG));
+                }
+            } else if (tid < 32 * it.z) { // thread (pair jp, row r): quantise the unit's 32 rows
+                const int jp = tid >> 5, r = tid & 31;
+                const float hv = silu_mul(s_gu[r * 8 + jp], s_gu[(32 + r) * 8 + jp]);
                 float amax = fabsf(hv);
 #pragma unroll
                 for (int off = 1; off < 32; off <<= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
                 float d;
                 const float id = quant_scale_inv(amax, d);
-                const unsigned q = (unsigned)(uint8_t)quant_one(hv, id);
-                const unsigned q1 = __shfl_down(q, 1, 64), q2 = __shfl_down(q, 2, 64), q3 = __shfl_down(q, 3, 64);
-                if (act) {
-                    const int p = s_pairs[it.y + jp];
-                    uint64_t *dstw = EX + EX_HQ + ((size_t)p * 16 + blk32) * 9;
-                    if ((rr & 3) == 0) ST_A(dstw + (rr >> 2), ((uint64_t)tagG << 32) | (q | (q1 << 8) | (q2 << 16) | (q3 << 24)));
-                    if (rr == 0) ST_A(dstw + 8, pack_tv(d, tagG));
+                const unsigned qv = (unsigned)(uint8_t)quant_one(hv, id);
+                const unsigned q1 = __shfl_down(qv, 1, 64), q2 = __shfl_down(qv, 2, 64), q3 = __shfl_down(qv, 3, 64);
+                const int p = s_pairs[it.y + jp];
+                uint64_t *dstw = EX + EX_HQ + ((size_t)p * 16 + j0 / 32) * 9;
+#pragma unroll
+                for (int rp = 0; rp < REP; ++rp) {
+                    if ((r & 3) == 0) ST_A(dstw + rp * EX_TOTAL + (r >> 2), ((uint64_t)tagG << 32) | (qv | (q1 << 8) | (q2 << 16) | (q3 << 24)));
+                    if (r == 0) ST_A(dstw + rp * EX_TOTAL + 8, pack_tv(d, tagG));
                 }
             }
-            __syncthreads(); // s_h is reused by the next unit
+            __syncthreads(); // s_gu is reused by the next unit
         }
+        d_prefetch(); // workgroups without a unit
         stage_arrive(CG);
 
         // ================= D: routed down + shared down + combine =================
         stage_wait(CG, (unsigned)li + 1u, a.err);
-        for (int task = tid; task < np * 16; task += 256) { // (pair, 32-block): 8 code words + 1 scale
-            const int p = task >> 4, b = task & 15;
-            const uint64_t *srcw = EX + EX_HQ + ((size_t)p * 16 + b) * 9;
-            uint64_t w[9];
-            for (int spins = 0;; ++spins) {
-#pragma unroll
-                for (int i = 0; i < 9; ++i) w[i] = LD_A((uint64_t *)srcw + i);
-                unsigned bad = 0;
-#pragma unroll
-                for (int i = 0; i < 9; ++i) bad |= (unsigned)(w[i] >> 32) ^ tagG;
-                if (__all(bad == 0)) break;
-                if (spins > SPIN_CAP) { ST_A(a.err, 1u); break; }
-                __builtin_amdgcn_s_sleep(1);
-            }
-            uint4 *dq = (uint4 *)(s_hq + p * QE_FF_EXP + b * 32);
-            dq[0] = make_uint4((unsigned)w[0], (unsigned)w[1], (unsigned)w[2], (unsigned)w[3]);
-            dq[1] = make_uint4((unsigned)w[4], (unsigned)w[5], (unsigned)w[6], (unsigned)w[7]);
-            s_hs[task] = tv_val(w[8]);
+        // shared-expert activations of every token: written in R, long landed by now
+        // (every workgroup has passed G); read once, tags verified
+        for (int i = tid; i < T * QE_FF_SH; i += NTH) {
+            uint64_t w[1];
+            read_tv<1>(EXr + EX_HSH + i, 0, tagR, w, true, a.err);
+            s_hsh[i] = tv_val(w[0]);
         }
-        __builtin_amdgcn_s_waitcnt(0); // this wave's global->LDS prefetch has landed
+        if (mode16) { // fp32 h of the 8 pairs -> LDS, then int8 per 32 rows
+            for (int i0 = 0; i0 < 8 * QE_FF_EXP; i0 += 2 * NTH) {
+                uint64_t w[2];
+                read_tv<2>(EXr + EX_HF + i0 + tid, NTH, tagG, w, true, a.err);
+                s_hf[i0 + tid] = tv_val(w[0]);
+                s_hf[i0 + tid + NTH] = tv_val(w[1]);
+            }
+            __syncthreads();
+            if (tid < 8 * 16) { // thread (pair, block)
+                float v[32];
+#pragma unroll
+                for (int i = 0; i < 32; ++i) v[i] = s_hf[tid * 32 + i];
+                lane_quant_store(v, s_hq + tid * 32, s_hs + tid);
+            }
+        } else {
+            for (int task = tid; task < np * 16; task += NTH) { // (pair, 32-block): 8 code words + 1 scale
+                const int p = task >> 4, b = task & 15;
+                uint64_t w[9];
+                read_tv<9>(EXr + EX_HQ + ((size_t)p * 16 + b) * 9, 1, tagG, w, true, a.err);
+                uint4 *dq = (uint4 *)(s_hq + p * QE_FF_EXP + b * 32);
+                dq[0] = make_uint4((unsigned)w[0], (unsigned)w[1], (unsigned)w[2], (unsigned)w[3]);
+                dq[1] = make_uint4((unsigned)w[4], (unsigned)w[5], (unsigned)w[6], (unsigned)w[7]);
+                s_hs[task] = tv_val(w[8]);
+            }
+        }
         __syncthreads();
         for (int m = 0; m < d_iters; ++m) {
             const int rb = (blockIdx.x + m * gridDim.x) * 8;
             if (rb >= QE_D) break;
-            const int r = rb + wv * 2 + rsel;
-            float y[DEC_T];
+            const int r = rb + rr;
+            float y[TM];
 #pragma unroll
-            for (int t = 0; t < DEC_T; ++t) y[t] = 0.f;
-            for (int u = half; u < nitems; u += 2) {
-                const int4 it = s_items[u];
+            for (int t = 0; t < TM; ++t) y[t] = 0.f;
+            for (int k = 0; half + 8 * k < nitems; ++k) {
+                const int s = 4 * k + isub, u = half + 2 * s;
+                const bool act = u < nitems;
+                const int4 it = s_items[act ? u : half];
                 uint4 q;
                 uint16_t sraw;
-                if (m == 0 && u < DEC_PFI) {
-                    q = s_dw[u * 32 + rsel * 16 + l16];
-                    sraw = (uint16_t)s_ds[u * 32 + rsel * 16 + l16];
+                if (m == 0 && k < 2) { // prefetched during G
+                    q = k == 0 ? dpq[0] : dpq[1];
+                    sraw = (uint16_t)(k == 0 ? dps[0] : dps[1]);
                 } else {
                     const uint8_t *drow = arena + (size_t)it.x * QE_EXPERT_BYTES + QE_EXPERT_DOWN_OFF + (size_t)r * QE_DN_ROW_BYTES;
                     q = *(const uint4 *)(drow + l16 * 16);
@@ -503,47 +648,66 @@ __global__ __launch_bounds__(256) void k_decode(QeDecodeArgs a) {
                 }
                 const nl4_blk w = nl4_decode_block(q);
                 const float sc = f16_bits_to_f32(sraw);
-                for (int j = 0; j < it.z; ++j) {
-                    const int p = s_pairs[it.y + j], tp = p / QE_K_USED;
+                const int npair = act ? it.z : 0;
+                for (int j = 0; j < T; ++j) { // pairs of the item (<= T); wave-uniform trip count
+                    const bool pj = j < npair;
+                    const int p = pj ? s_pairs[it.y + j] : 0, tp = p / QE_K_USED;
                     const int8_t *hq = s_hq + p * QE_FF_EXP + l16 * 32;
                     const int P = nl4_block_dot(w, *(const uint4 *)hq, *(const uint4 *)(hq + 16));
-                    float v = (sc * s_hs[p * 16 + l16]) * (float)P;
-                    v = sum16(v) * s_wts[p];
+                    const float v = sum16((sc * s_hs[p * 16 + l16]) * (float)P);
+                    const float vw = pj ? v * s_wts[p] : 0.f;
 #pragma unroll
-                    for (int t = 0; t < DEC_T; ++t) y[t] += t == tp ? v : 0.f;
+                    for (int t = 0; t < TM; ++t) y[t] += t == tp ? vw : 0.f;
                 }
             }
 #pragma unroll
-            for (int t = 0; t < DEC_T; ++t) y[t] = y[t] + __shfl_xor(y[t], 16, 64);
-            if (m > 0) {
-                const uint8_t *srow = sh_dn + (size_t)r * QE_SH_DN_ROW_BYTES;
-                dq0 = ((const uint4 *)(srow + l16 * 32))[0];
-                dq1 = ((const uint4 *)(srow + l16 * 32))[1];
-                dsc = ((const uint16_t *)(srow + QE_FF_SH))[l16];
+            for (int t = 0; t < TM; ++t) {
+                y[t] = y[t] + __shfl_xor(y[t], 16, 64);
+                y[t] = y[t] + __shfl_xor(y[t], 32, 64);
             }
-            float w8[32];
-            unpack_i8x32(dq0, dq1, w8);
-            const float ssd = f16_bits_to_f32(dsc);
-            for (int t = 0; t < T; ++t) {
-                float acc = 0.f;
+            if (lane == 0) {
 #pragma unroll
-                for (int i = 0; i < 32; ++i) acc = fmaf(w8[i], s_hsh[t * QE_FF_SH + l16 * 32 + i], acc);
-                const float sd = sum16(acc * ssd);
-                float yt = y[0];
+                for (int t = 0; t < TM; ++t)
+                    if (t < T) s_y[(rr * 2 + half) * DEC_T + t] = y[t];
+            }
+            if (half == 0) { // shared down row r: 16-lane group g takes tokens g, g + 4
+                if (m > 0) {
+                    const uint8_t *srow = sh_dn + (size_t)r * QE_SH_DN_ROW_BYTES;
+                    dq0 = ((const uint4 *)(srow + l16 * 32))[0];
+                    dq1 = ((const uint4 *)(srow + l16 * 32))[1];
+                    dsc = ((const uint16_t *)(srow + QE_FF_SH))[l16];
+                }
+                float w8[32];
+                unpack_i8x32(dq0, dq1, w8);
+                const float ssd = f16_bits_to_f32(dsc);
+                for (int t0 = 0; t0 < T; t0 += 4) {
+                    const int t = t0 + isub;
+                    float acc = 0.f;
+                    if (t < T) {
 #pragma unroll
-                for (int k = 1; k < DEC_T; ++k) yt = t == k ? y[k] : yt;
-                if ((lane & 31) == 0) {
-                    const size_t o = (size_t)t * QE_D + r;
-                    const float res = a.residual ? s_res[t * 32 + m * 8 + (r - rb)] : 0.f;
-                    const float out = (res + s_shg[t] * sd) + yt;
-                    if (last) {
-                        a.x_out[o] = out;
-                        if (a.sd_out) a.sd_out[o] = sd;
-                    } else {
-                        ST_A(dst_x + o, pack_tv(out, tagD));
+                        for (int i = 0; i < 32; ++i) acc = fmaf(w8[i], s_hsh[t * QE_FF_SH + l16 * 32 + i], acc);
                     }
+                    const float sd = sum16(acc * ssd);
+                    if (l16 == 0 && t < T) s_y[16 * DEC_T + rr * DEC_T + t] = sd;
                 }
             }
+            __syncthreads();
+            if (tid < 8 * T) { // thread (row, token): combine
+                const int k = tid / T, t = tid % T, ro = rb + k;
+                const float sd = s_y[16 * DEC_T + k * DEC_T + t];
+                const float yt = s_y[(k * 2) * DEC_T + t] + s_y[(k * 2 + 1) * DEC_T + t];
+                const float res = a.residual ? s_res[t * 32 + m * 8 + k] : 0.f;
+                const float out = (res + s_shg[t] * sd) + yt;
+                const size_t o = (size_t)t * QE_D + ro;
+                if (last) {
+                    a.x_out[o] = out;
+                    if (a.sd_out) a.sd_out[o] = sd;
+                } else {
+#pragma unroll
+                    for (int r = 0; r < REP; ++r) ST_A(dst_x + r * EX_TOTAL + o, pack_tv(out, tagD));
+                }
+            }
+            __syncthreads(); // s_y is rewritten by the next row group
         }
         if (!last) stage_arrive(CD);
         __syncthreads(); // the LDS union is rewritten by the next layer's R stage
@@ -553,28 +717,33 @@ __global__ __launch_bounds__(256) void k_decode(QeDecodeArgs a) {
     // so the next launch starts from zero counts with new tags
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    if (tid == 0 && ADD_A(a.sync + SYNC_EXIT, 1u) == gridDim.x - 1) {
-        for (int i = 0; i < 3 * 16; ++i) ST_A(a.sync + SYNC_CTR + i * 32, 0u);
+    if (threadIdx.x == 0 && ADD_A(a.sync + SYNC_EXIT, 1u) == gridDim.x - 1) {
+        for (int i = 0; i < REP * 3 * 16; ++i) ST_A(a.sync + SYNC_CTR + i * 32, 0u);
         ST_A(a.sync + SYNC_EXIT, 0u);
         ST_A(a.sync + SYNC_EPOCH, epoch + 1u);
     }
 }
 
-hipError_t qe_launch_decode(const QeDecodeArgs &a, hipStream_t st) {
+template <int TM> static hipError_t launch_decode(const QeDecodeArgs &a, hipStream_t st) {
     static int grid = 0;
     if (!grid) {
-        hipError_t e = hipFuncSetAttribute((const void *)k_decode, hipFuncAttributeMaxDynamicSharedMemorySize, L_TOTAL);
+        hipError_t e = hipFuncSetAttribute((const void *)k_decode<TM>, hipFuncAttributeMaxDynamicSharedMemorySize, L_TOTAL);
         if (e != hipSuccess) return e;
         int dev = 0, cus = 0, per_cu = 0;
         if ((e = hipGetDevice(&dev)) != hipSuccess) return e;
         if ((e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev)) != hipSuccess) return e;
-        if ((e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_decode, 256, L_TOTAL)) != hipSuccess) return e;
+        if ((e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_decode<TM>, NTH, L_TOTAL)) != hipSuccess) return e;
         if (per_cu < 1) return hipErrorInvalidConfiguration;
-        // one workgroup per CU, 64..256 of them (stage counters cover 16 groups of 16; D
-        // rows per workgroup stay within the 32-row residual buffer)
+        // one workgroup per CU, 64..256 of them (stage counters cover 16 groups of 16; a
+        // workgroup's D rows, <= 4 groups of 8, stay within the 32-row residual buffer)
         grid = cus < 256 ? cus : 256;
         if (grid < DEC_MIN_GRID) return hipErrorInvalidConfiguration;
     }
     void *args[] = {(void *)&a};
-    return hipLaunchCooperativeKernel((const void *)k_decode, dim3(grid), dim3(256), args, L_TOTAL, st);
+    return hipLaunchCooperativeKernel((const void *)k_decode<TM>, dim3(grid), dim3(NTH), args, L_TOTAL, st);
+}
+
+hipError_t qe_launch_decode(const QeDecodeArgs &a, hipStream_t st) {
+    if (a.T < 1 || a.T > DEC_T) return hipErrorInvalidValue;
+    return a.T == 1 ? launch_decode<1>(a, st) : launch_decode<DEC_T>(a, st);
 }

@@ -208,7 +208,7 @@ QE_DEV void lane_quant_store(const float v[32], int8_t *q_out, float *s_out) {
 // of 32-blocks (2q, 2q+1), 64 bytes = 4 groups g of 16 bytes; group g holds
 // 8 bytes of block 2q then 8 of block 2q+1, each run being elements
 // 4g..4g+3 followed by 16+4g..16+4g+3 of its block.
-QE_HD inline int qe_opnd_off(int k) {
+QE_HD int qe_opnd_off(int k) {
     const int b = k >> 5, e = k & 31;
     return (b >> 1) * 64 + ((e & 15) >> 2) * 16 + (b & 1) * 8 + (e >> 4) * 4 + (e & 3);
 }

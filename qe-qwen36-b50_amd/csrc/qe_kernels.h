@@ -81,11 +81,12 @@ struct QeDecodeArgs {
     uint64_t *ex;        // exchange words {value, tag}, QE_DECODE_EX_WORDS of them (qe_decode.hip)
     // routing sink of the last layer (plain stores by workgroup 0)
     float *logits; int32_t *ids; float *wts; float *shg; int32_t *off; int32_t *pairs; float *sd_out; float *xn_out;
-    unsigned *sync;      // [0] launch epoch, [32] exit counter, [64..832) stage flags
+    unsigned *sync;      // QE_DECODE_SYNC_WORDS: [0] launch epoch, [32] exit counter, [64..) stage counters
     unsigned *err;       // set to 1 if a poll timed out
 };
 hipError_t qe_launch_decode(const QeDecodeArgs &a, hipStream_t st);
-#define QE_DECODE_EX_WORDS (2 * QE_SMALL_T * QE_D + QE_SMALL_T * QE_ROUTER_ROWS + QE_SMALL_T * QE_FF_SH + QE_SMALL_T * 8 * 16 * 9)
+#define QE_DECODE_EX_WORDS (8 * (2 * QE_SMALL_T * QE_D + QE_SMALL_T * QE_ROUTER_ROWS + QE_SMALL_T * QE_FF_SH + QE_SMALL_T * 8 * 16 * 9 + 8 * QE_FF_EXP))
+#define QE_DECODE_SYNC_WORDS 16384 /* epoch, exit counter, 8 x 3 x 16 stage counters 128 B apart */
 
 // Launchers (qe_kernels.hip).  xin: layer input; post_norm: nullptr = input is
 // already normalised; x2: residual added to the output or nullptr.
