@@ -42,7 +42,7 @@
 #define SYNC_EPOCH 0
 #define SYNC_EXIT 32
 #define SYNC_CTR 64       /* per replica: 3 stages x 16 groups, 32 words apart: (unused), G, D */
-#define REP 8             /* copies of every exchanged buffer and counter */
+#define REP QE_DEC_REP      /* copies of every exchanged buffer and counter */
 #define CTR_REP (3 * 16 * 32)
 #define SPIN_CAP (1 << 22)
 #define DEC_MIN_GRID 64   /* D row groups per workgroup stay <= 4 */

@@ -85,8 +85,12 @@ struct QeDecodeArgs {
     unsigned *err;       // set to 1 if a poll timed out
 };
 hipError_t qe_launch_decode(const QeDecodeArgs &a, hipStream_t st);
-#define QE_DECODE_EX_WORDS (8 * (2 * QE_SMALL_T * QE_D + QE_SMALL_T * QE_ROUTER_ROWS + QE_SMALL_T * QE_FF_SH + QE_SMALL_T * 8 * 16 * 9 + 8 * QE_FF_EXP))
-#define QE_DECODE_SYNC_WORDS 16384 /* epoch, exit counter, 8 x 3 x 16 stage counters 128 B apart */
+#ifndef QE_DEC_REP
+#define QE_DEC_REP 8 /* copies of every decode exchange buffer and stage counter */
+#endif
+#define QE_DECODE_EX_WORDS \
+    (QE_DEC_REP * (2 * QE_SMALL_T * QE_D + QE_SMALL_T * QE_ROUTER_ROWS + QE_SMALL_T * QE_FF_SH + QE_SMALL_T * 8 * 16 * 9 + 8 * QE_FF_EXP))
+#define QE_DECODE_SYNC_WORDS (64 + QE_DEC_REP * 3 * 16 * 32) /* epoch, exit counter, stage counters 128 B apart */
 
 // Launchers (qe_kernels.hip).  xin: layer input; post_norm: nullptr = input is
 // already normalised; x2: residual added to the output or nullptr.
