@@ -40,8 +40,12 @@ extern "C" {
 
 typedef struct qe_moe_ctx qe_moe_ctx;
 
+/* Largest t_max a context accepts (prefill scratch offsets stay 32-bit). */
+#define QE_MOE_T_MAX 65536
+
 /* Create a context on `device` for n_layers layers and calls of up to t_max
- * tokens.  Allocates the arena (n_layers * 452,984,832 B) and scratch.
+ * tokens (1..QE_MOE_T_MAX).  Allocates the arena (n_layers * 452,984,832 B)
+ * and scratch.
  * Replaces Engine::Engine's upload/arena/scratch set-up (engine/qe.cpp:1038-1244). */
 int qe_moe_create(int device, int n_layers, int t_max, qe_moe_ctx **out);
 int qe_moe_destroy(qe_moe_ctx *ctx);

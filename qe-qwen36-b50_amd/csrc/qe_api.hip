@@ -53,6 +53,9 @@ static int dalloc(qe_moe_ctx *c, void **p, size_t bytes) {
         return fail(QE_ERR_OOM, "hipMalloc(%zu) failed", bytes);
     }
     c->allocs.push_back(*p);
+    // scratch starts as zeros: the padding rows of the prefill tiles are read
+    // (never stored), and must hold finite values
+    if (hipMemset(*p, 0, bytes) != hipSuccess) return fail(QE_ERR_HIP, "hipMemset(%zu) failed", bytes);
     return QE_OK;
 }
 
@@ -79,7 +82,7 @@ const char *qe_moe_last_error(void) { return g_err.c_str(); }
 size_t qe_moe_expert_bytes(void) { return QE_EXPERT_BYTES; }
 
 int qe_moe_create(int device, int n_layers, int t_max, qe_moe_ctx **out) {
-    if (!out || n_layers <= 0 || n_layers > 4096 || t_max <= 0 || t_max > (1 << 20))
+    if (!out || n_layers <= 0 || n_layers > 4096 || t_max <= 0 || t_max > QE_MOE_T_MAX)
         return fail(QE_ERR_ARG, "qe_moe_create: bad argument (n_layers=%d t_max=%d)", n_layers, t_max);
     *out = nullptr;
     HIP_TRY(hipSetDevice(device));
@@ -89,7 +92,7 @@ int qe_moe_create(int device, int n_layers, int t_max, qe_moe_ctx **out) {
     c->t_max = t_max;
     c->has_bias.assign(n_layers, 0);
     c->ready.assign(n_layers, 0);
-    const size_t L = (size_t)n_layers, T = (size_t)t_max, NP = T * QE_K_USED;
+    const size_t L = (size_t)n_layers, T = (size_t)t_max, NP = T * QE_K_USED, T32 = (T + 31) & ~(size_t)31;
     const size_t max_items = NP / QE_MFMA_MC + QE_N_EXPERT;
     const size_t nch = (NP + 1023) / 1024;
     int rc = QE_OK;
@@ -105,8 +108,9 @@ int qe_moe_create(int device, int n_layers, int t_max, qe_moe_ctx **out) {
     A(S.xn, T * QE_D * 4);
     A(S.xqp, T * QE_D);
     A(S.xs, T * (QE_D / 32) * 4);
+    A(S.xhl, T32 * QE_D * 4);
     A(S.logits, T * QE_ROUTER_ROWS * 4);
-    A(S.shgu, T * QE_SH_GU_ROWS * 4);
+    A(S.shgu, T32 * QE_FF_SH * 4);
     A(S.rpart, 4 * T * QE_ROUTER_ROWS * 4);
     A(S.ids, NP * 4);
     A(S.wts, NP * 4);

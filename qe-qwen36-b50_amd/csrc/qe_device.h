@@ -233,6 +233,42 @@ QE_DEV void lane_quant_store_opnd(const float v[32], int8_t *row, int b, float *
     *s_out = d;
 }
 
+// fp32 activations for the fp16 matrix cores: a = a_hi + a_lo with
+// a_hi = fp16(a), a_lo = fp16(a - a_hi) (the difference is exact in fp32), so
+// a_hi + a_lo carries ~22 significant bits for |a| < 65504.
+// Rows are stored in the operand order of v_mfma_f32_32x32x16_f16, 32 rows per
+// tile: per 32-block b, four 1 KB chunks q of 64 lanes x 16 B, where lane
+// l = r + 32 kh (row r of the tile) holds, for q = 0..3: hi of block elements
+// 16 kh + 0..7, hi of 16 kh + 8..15, lo of 16 kh + 0..7, lo of 16 kh + 8..15.
+// One dwordx4 load per lane and chunk reads 1 KB contiguous.  Byte offset of
+// the hi half of element k of row `row` (K elements per row); lo is 2048 B on.
+QE_HD size_t qe_hl_off(int K, int row, int k) {
+    const int e = k & 31;
+    return ((((size_t)(row >> 5) * (K / 32) + (k >> 5)) * 4 + ((e >> 3) & 1)) * 64 + (row & 31) + 32 * (e >> 4)) * 16 +
+           2 * (e & 7);
+}
+#define QE_HL_LO 2048
+QE_DEV uint32_t pack_h2(_Float16 a, _Float16 b) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+}
+// Split the 32 values of block b of row `row` and store them in that layout.
+QE_DEV void store_hilo_block(const float v[32], uint8_t *base, int K, int row, int b) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) { // 8 consecutive elements 8g..8g+7
+        uint32_t h[4], l[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float x0 = v[8 * g + 2 * i], x1 = v[8 * g + 2 * i + 1];
+            const _Float16 a0 = (_Float16)x0, a1 = (_Float16)x1;
+            h[i] = pack_h2(a0, a1);
+            l[i] = pack_h2((_Float16)(x0 - (float)a0), (_Float16)(x1 - (float)a1));
+        }
+        uint8_t *dst = base + qe_hl_off(K, row, 32 * b + 8 * g);
+        *(uint4 *)dst = make_uint4(h[0], h[1], h[2], h[3]);
+        *(uint4 *)(dst + QE_HL_LO) = make_uint4(l[0], l[1], l[2], l[3]);
+    }
+}
+
 QE_DEV void load32(const float *p, float v[32]) {
     const float4 *q = (const float4 *)p;
 #pragma unroll

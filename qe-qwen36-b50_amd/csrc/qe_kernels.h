@@ -5,7 +5,7 @@
 
 #include "qe_device.h"
 
-#define QE_SMALL_T 8   /* tokens per call handled by the 3-launch small-T plan */
+#define QE_SMALL_T 8   /* calls of up to this many tokens take the persistent decode kernel */
 #define QE_MFMA_MC 32 /* pairs per work item of the prefill MFMA grouped GEMMs (two 16-row tiles) */
 
 
@@ -50,8 +50,9 @@ struct ProfScope {
 // Scratch of a context, sized for t_max tokens.
 struct QeScratch {
     float *xn; int8_t *xqp; float *xs;      // [T][2048] normed x, its int8 quantisation (operand layout), [T][64] scales
+    _Float16 *xhl;                          // [T][2048] normed x as fp16 hi|lo halves (store_hilo16 layout)
     float *logits;                          // [T][257]
-    float *shgu;                            // [T][1024] (decode: unused) / [T][512] shared silu(g)*u (prefill)
+    float *shgu;                            // prefill: shared silu(g)*u as [T][512] fp16 hi|lo halves
     float *rpart;                           // [4][T][257] router subtree partials
     int32_t *ids; float *wts; float *shg;   // [T][8], [T][8], [T]
     int32_t *off; int32_t *pairs;           // [257], [T*8]

@@ -16,7 +16,7 @@
 // ===========================================================================
 // wave per token: xn, xq, xs
 __global__ __launch_bounds__(256) void k_normq(const float *x, int T, const float *post_norm, float *xn, int8_t *xqp,
-                                               float *xs) {
+                                               float *xs, _Float16 *xhl) {
     const int lane = threadIdx.x & 63, t = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (t >= T) return;
     float v[32];
@@ -25,6 +25,7 @@ __global__ __launch_bounds__(256) void k_normq(const float *x, int T, const floa
     float4 *xo = (float4 *)(xn + (size_t)t * QE_D + lane * 32);
 #pragma unroll
     for (int i = 0; i < 8; ++i) xo[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+    store_hilo_block(v, (uint8_t *)xhl, QE_D, t, lane);
     lane_quant_store_opnd(v, xqp + (size_t)t * QE_D, lane, xs + (size_t)t * (QE_D / 32) + lane);
 }
 
@@ -274,7 +275,7 @@ hipError_t qe_launch_layer(const QeLayerPtrs &L, const QeScratch &S, const float
     const int mt = (T + 63) / 64;
     {
         QE_PROF(QP_NORMQ);
-        k_normq<<<(T + 3) / 4, 256, 0, st>>>(xin, T, pn, S.xn, S.xqp, S.xs);
+        k_normq<<<(T + 3) / 4, 256, 0, st>>>(xin, T, pn, S.xn, S.xqp, S.xs, S.xhl);
     }
     {
         QE_PROF(QP_ROUTER);

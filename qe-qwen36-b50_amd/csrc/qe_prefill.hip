@@ -17,7 +17,6 @@
 #include "qe_kernels.h"
 
 typedef _Float16 qe_half8 __attribute__((ext_vector_type(8)));
-typedef float qe_float16v __attribute__((ext_vector_type(16)));
 
 
 // fp16 of small integers: half(0x6400 | u) = 1024 + u for u in 0..1023, so a
@@ -347,110 +346,150 @@ hipError_t qe_launch_expert_mfma(const QeLayerPtrs &L, const QeScratch &S, int T
 
 // ===========================================================================
 // Shared expert (Q8 weights, fp32 activations; engine/qe.cpp:2469, :1656,
-// :1960-1963) as MFMA GEMMs.  Q8 values are exact in fp16; an fp32
-// activation a is split into fp16 a_hi = fp16(a) and a_lo = fp16(a - a_hi), so
-// two MFMA chains into one accumulator give sum (a_hi + a_lo) w, within ~2^-22
-// of the fp32 product (activation magnitudes below 65504).  The per-block Q8
-// scale is applied in a one-fma epilogue.
-//   gate_up: A = xn [T][2048], N-tile = gate rows j0..j0+63 (waves 0,1) and up
-//            rows j0..j0+63 (waves 2,3), output h_sh[T][512] = silu(g) * u.
-//   down:    A = h_sh [T][512], N-tile = 128 down rows, output sd[T][2048].
-// Workgroup = 32 tokens x 128 columns, 32 columns per wave.
+// :1960-1963) as fp16 MFMA GEMMs.  The activations arrive split into fp16
+// hi + lo halves in the interleaved layout of store_hilo16 (k_normq writes xn
+// that way, the gate/up epilogue writes h); Q8 values are exact in fp16, so two
+// MFMA chains (hi, lo) give each 32-block dot within ~2^-22 of fp32, and the
+// block's Q8 scale is one fma per output.
+//
+// v_mfma_f32_32x32x16_f16: lane l supplies 8 k of row (A) / column (B) l % 32
+// and receives D[8 (i / 4) + 4 (l / 32) + i % 4][l % 32], i = 0..15.  Within a
+// 32-block, lane (., kh = l / 32) feeds elements 16 kh + 8 s + 0..7 at step
+// s = 0, 1 on both operands -- a permutation of the block's k, so the same dot.
+// The activations are stored in exactly that order (qe_hl_off), so each of a
+// lane's four A chunks per block is one 1 KB-contiguous dwordx4 load, and its
+// B operand is one 16-byte run of a Q8 row.
+//   gate/up: workgroup = 32 tokens x (gate rows j0..j0+31, up rows j0..j0+31),
+//            the four waves split K in quarters, partial sums meet in LDS,
+//            h = silu(g) * u is written as hi|lo halves.
+//   down:    workgroup = 32 tokens x 128 output rows, 32 per wave, full K.
+// Rows T..T+31 of the last tile exist in the buffers (sized for whole tiles) and
+// are never stored; each output row depends on its own A row only.
 // ===========================================================================
-QE_DEV void f32x8_to_hilo(const float4 v0, const float4 v1, qe_half8 &hi, qe_half8 &lo) {
-    const float f[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+typedef float qe_float16v __attribute__((ext_vector_type(16)));
+#define SH_GU_KB 16 /* 32-blocks per wave in gate/up: 2048 / 32 / 4 */
+
+QE_DEV qe_u32x4 sh_ld(__amdgpu_buffer_rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0); }
+
+// one 32-block: acc += dw * (A_hi + A_lo) . B, A = a[0..3] (hi 0..7, hi 8..15, lo 0..7, lo 8..15)
+QE_DEV void sh_block(const qe_u32x4 a[4], qe_u32x4 w, float dw, qe_float16v &acc) {
+    const qe_half8 b0 = i8x8_to_half8(w.x, w.y), b1 = i8x8_to_half8(w.z, w.w);
+    qe_float16v p = {};
+    p = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(qe_half8, a[0]), b0, p, 0, 0, 0);
+    p = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(qe_half8, a[2]), b0, p, 0, 0, 0);
+    p = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(qe_half8, a[1]), b1, p, 0, 0, 0);
+    p = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(qe_half8, a[3]), b1, p, 0, 0, 0);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const _Float16 h = (_Float16)f[j];
-        hi[j] = h;
-        lo[j] = (_Float16)(f[j] - (float)h);
+    for (int i = 0; i < 16; ++i) acc[i] = fmaf(dw, p[i], acc[i]);
+}
+QE_DEV float half_of(const qe_u32x4 s[2], int b) { // fp16 scale b of 16 packed in two dwordx4
+    const uint32_t w = s[b >> 3][(b >> 1) & 3];
+    return f16_bits_to_f32((uint16_t)((b & 1) ? w >> 16 : w & 0xffffu));
+}
+
+__global__ __launch_bounds__(256) void k_shared_gu(const _Float16 *xhl, int T, const uint8_t *W, _Float16 *hhl) {
+    constexpr uint32_t RB = QE_SH_GU_ROW_BYTES;
+    __shared__ float red[4][2][16][64];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, c = lane & 31, kh = lane >> 5;
+    const int m0 = blockIdx.x * 32, j0 = blockIdx.y * 32, kb0 = wv * SH_GU_KB;
+    const __amdgpu_buffer_rsrc_t ra =
+        __builtin_amdgcn_make_buffer_rsrc((void *)xhl, (short)0, ((T + 31) & ~31) * QE_D * 4, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void *)W, (short)0, (int)QE_SH_GU_BYTES, 0x00020000);
+    const uint32_t a_off = (uint32_t)(blockIdx.x * (QE_D / 32) + kb0) * 4096 + lane * 16;
+    const uint32_t g_off = (uint32_t)(j0 + c) * RB, u_off = g_off + QE_FF_SH * RB;
+    qe_u32x4 sg[2], su[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        sg[i] = sh_ld(rw, g_off + QE_D + 2 * kb0 + 16 * i);
+        su[i] = sh_ld(rw, u_off + QE_D + 2 * kb0 + 16 * i);
+    }
+    qe_float16v ag = {}, au = {};
+    constexpr int DEPTH = 4;
+    qe_u32x4 ra_[DEPTH][4], rg[DEPTH], ru[DEPTH];
+    auto load = [&](int b) {
+        const int s = b % DEPTH;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) ra_[s][q] = sh_ld(ra, a_off + 4096 * b + 1024 * q);
+        rg[s] = sh_ld(rw, g_off + 32 * (kb0 + b) + 16 * kh);
+        ru[s] = sh_ld(rw, u_off + 32 * (kb0 + b) + 16 * kh);
+    };
+#pragma unroll
+    for (int b = 0; b < DEPTH; ++b) load(b);
+#pragma unroll
+    for (int b = 0; b < SH_GU_KB; ++b) {
+        const int s = b % DEPTH;
+        const qe_u32x4 a[4] = {ra_[s][0], ra_[s][1], ra_[s][2], ra_[s][3]};
+        const qe_u32x4 wg = rg[s], wu = ru[s];
+        if (b + DEPTH < SH_GU_KB) load(b + DEPTH);
+        sh_block(a, wg, half_of(sg, b), ag);
+        sh_block(a, wu, half_of(su, b), au);
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        red[wv][0][i][lane] = ag[i];
+        red[wv][1][i][lane] = au[i];
+    }
+    __syncthreads();
+    // thread: lane L of the accumulators, i = 4 (tid / 64) .. +3 -> 4 (token, j) outputs
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int i = 4 * wv + q;
+        const float g = (red[0][0][i][lane] + red[1][0][i][lane]) + (red[2][0][i][lane] + red[3][0][i][lane]);
+        const float u = (red[0][1][i][lane] + red[1][1][i][lane]) + (red[2][1][i][lane] + red[3][1][i][lane]);
+        const int m = m0 + 8 * (i >> 2) + 4 * kh + (i & 3), j = j0 + c;
+        if (m < T) {
+            const float h = silu_mul(g, u);
+            const _Float16 hi = (_Float16)h, lo = (_Float16)(h - (float)hi);
+            uint8_t *dst = (uint8_t *)hhl + qe_hl_off(QE_FF_SH, m, j);
+            *(_Float16 *)dst = hi;
+            *(_Float16 *)(dst + QE_HL_LO) = lo;
+        }
     }
 }
-// 8 int8 (two dwords) -> 8 fp16, exact
-QE_DEV qe_half8 q8x8_to_half8(uint32_t lo, uint32_t hi) { return i8x8_to_half8(lo, hi); }
 
-template <bool GU>
-__global__ __launch_bounds__(256) void k_shared_mfma(const float *A, int T, const uint8_t *W, float *out) {
-    constexpr int KD = GU ? QE_D : QE_FF_SH;
-    constexpr int NB = KD / 32;
-    constexpr size_t RB = (size_t)KD + KD / 32 * 2;
-    __shared__ float s_up[2][16][64];
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, l32 = lane & 31, kq = lane >> 5;
-    const int m0 = blockIdx.x * 32;
-    // this wave's 32 columns
-    int row;
-    if (GU) row = (wv < 2 ? 0 : QE_FF_SH) + blockIdx.y * 64 + (wv & 1) * 32 + l32;
-    else row = blockIdx.y * 128 + wv * 32 + l32;
-    const uint8_t *wrow = W + (size_t)row * RB;
-    const int m = m0 + l32;
-    const float *arow = m < T ? A + (size_t)m * KD : nullptr;
-
-    qe_float16v acc;
+__global__ __launch_bounds__(256) void k_shared_dn(const _Float16 *hhl, int T, const uint8_t *W, float *out) {
+    constexpr uint32_t RB = QE_SH_DN_ROW_BYTES;
+    constexpr int NB = QE_FF_SH / 32;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, c = lane & 31, kh = lane >> 5;
+    const int m0 = blockIdx.x * 32, n = blockIdx.y * 128 + wv * 32 + c;
+    const __amdgpu_buffer_rsrc_t ra =
+        __builtin_amdgcn_make_buffer_rsrc((void *)hhl, (short)0, ((T + 31) & ~31) * QE_FF_SH * 4, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void *)W, (short)0, (int)QE_SH_DN_BYTES, 0x00020000);
+    const uint32_t a_off = (uint32_t)blockIdx.x * NB * 4096 + lane * 16;
+    const uint32_t w_off = (uint32_t)n * RB;
+    qe_u32x4 sw[2];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) acc[i] = 0.f;
-    float4 a_nx[4];
-    uint2 w_nx[2];
-    uint16_t s_nx;
-    auto fetch = [&](int b) {
+    for (int i = 0; i < 2; ++i) sw[i] = sh_ld(rw, w_off + QE_FF_SH + 16 * i);
+    qe_float16v acc = {};
+    constexpr int DEPTH = 4;
+    qe_u32x4 ra_[DEPTH][4], rb[DEPTH];
+    auto load = [&](int b) {
+        const int s = b % DEPTH;
 #pragma unroll
-        for (int s = 0; s < 2; ++s) {
-            const int k0 = b * 32 + 16 * s + 8 * kq;
-            if (arow) {
-                a_nx[2 * s] = *(const float4 *)(arow + k0);
-                a_nx[2 * s + 1] = *(const float4 *)(arow + k0 + 4);
-            } else {
-                a_nx[2 * s] = make_float4(0.f, 0.f, 0.f, 0.f);
-                a_nx[2 * s + 1] = a_nx[2 * s];
-            }
-            w_nx[s] = *(const uint2 *)(wrow + k0);
-        }
-        s_nx = ((const uint16_t *)(wrow + KD))[b];
+        for (int q = 0; q < 4; ++q) ra_[s][q] = sh_ld(ra, a_off + 4096 * b + 1024 * q);
+        rb[s] = sh_ld(rw, w_off + 32 * b + 16 * kh);
     };
-    fetch(0);
+#pragma unroll
+    for (int b = 0; b < DEPTH; ++b) load(b);
+#pragma unroll
     for (int b = 0; b < NB; ++b) {
-        float4 av[4] = {a_nx[0], a_nx[1], a_nx[2], a_nx[3]};
-        const uint2 wv2[2] = {w_nx[0], w_nx[1]};
-        const float dw = f16_bits_to_f32(s_nx);
-        if (b + 1 < NB) fetch(b + 1);
-        qe_float16v p = {};
-#pragma unroll
-        for (int s = 0; s < 2; ++s) {
-            qe_half8 hi, lo;
-            f32x8_to_hilo(av[2 * s], av[2 * s + 1], hi, lo);
-            const qe_half8 bf = q8x8_to_half8(wv2[s].x, wv2[s].y);
-            p = __builtin_amdgcn_mfma_f32_32x32x16_f16(hi, bf, p, 0, 0, 0);
-            p = __builtin_amdgcn_mfma_f32_32x32x16_f16(lo, bf, p, 0, 0, 0);
-        }
-#pragma unroll
-        for (int i = 0; i < 16; ++i) acc[i] = fmaf(dw, p[i], acc[i]);
+        const int s = b % DEPTH;
+        const qe_u32x4 a[4] = {ra_[s][0], ra_[s][1], ra_[s][2], ra_[s][3]};
+        const qe_u32x4 w = rb[s];
+        if (b + DEPTH < NB) load(b + DEPTH);
+        sh_block(a, w, half_of(sw, b), acc);
     }
-    // lane holds rows m0 + 8 (i / 4) + 4 kq + (i % 4) of column `row`
-    if (GU) {
-        if (wv >= 2) {
 #pragma unroll
-            for (int i = 0; i < 16; ++i) s_up[wv - 2][i][lane] = acc[i];
-        }
-        __syncthreads();
-        if (wv < 2) {
-            const int j = blockIdx.y * 64 + wv * 32 + l32;
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const int mm = m0 + 8 * (i / 4) + 4 * kq + (i % 4);
-                if (mm < T) out[(size_t)mm * QE_FF_SH + j] = silu_mul(acc[i], s_up[wv][i][lane]);
-            }
-        }
-    } else {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int mm = m0 + 8 * (i / 4) + 4 * kq + (i % 4);
-            if (mm < T) out[(size_t)mm * QE_D + row] = acc[i];
-        }
+    for (int i = 0; i < 16; ++i) {
+        const int m = m0 + 8 * (i >> 2) + 4 * kh + (i & 3);
+        if (m < T) out[(size_t)m * QE_D + n] = acc[i];
     }
 }
 
 hipError_t qe_launch_shared_mfma(const QeLayerPtrs &L, const QeScratch &S, int T, bool gate_up, hipStream_t st) {
     const unsigned mt = (unsigned)((T + 31) / 32);
-    if (gate_up) k_shared_mfma<true><<<dim3(mt, QE_FF_SH / 64), 256, 0, st>>>(S.xn, T, L.sh_gu, S.shgu);
-    else k_shared_mfma<false><<<dim3(mt, QE_D / 128), 256, 0, st>>>(S.shgu, T, L.sh_dn, S.sd);
+    _Float16 *hhl = (_Float16 *)S.shgu;
+    if (gate_up) k_shared_gu<<<dim3(mt, QE_FF_SH / 32), 256, 0, st>>>(S.xhl, T, L.sh_gu, hhl);
+    else k_shared_dn<<<dim3(mt, QE_D / 128), 256, 0, st>>>(hhl, T, L.sh_dn, S.sd);
     return hipGetLastError();
 }
