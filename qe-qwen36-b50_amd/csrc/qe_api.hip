@@ -111,7 +111,7 @@ int qe_moe_create(int device, int n_layers, int t_max, qe_moe_ctx **out) {
     A(S.xhl, T32 * QE_D * 4);
     A(S.logits, T * QE_ROUTER_ROWS * 4);
     A(S.shgu, T32 * QE_FF_SH * 4);
-    A(S.rpart, 4 * T * QE_ROUTER_ROWS * 4);
+    A(S.rpart, 8 * T * QE_N_EXPERT * 4);
     A(S.ids, NP * 4);
     A(S.wts, NP * 4);
     A(S.shg, T * 4);
@@ -297,9 +297,9 @@ int qe_moe_get_logits(qe_moe_ctx *c, int T, float *logits, void *stream) {
 }
 
 static const char *const k_prof_names[QP_N] = {
-    "k_decode", "k_normq", "k_router_split+k_router_combine", "k_shared_mfma<gate_up>", "k_topk",
+    "k_decode", "k_normq", "k_router_split", "k_shared_gu", "k_topk",
     "k_disp_hist+k_disp_scatter", "k_expert_mfma<gate_up>+k_expert_mfma<down>", "unused", "unused",
-    "k_shared_mfma<down>", "k_combine"};
+    "k_shared_dn", "k_combine"};
 
 int qe_moe_profile(qe_moe_ctx *c, int enable) {
     if (!c) return fail(QE_ERR_ARG, "profile: bad argument");

@@ -53,7 +53,7 @@ struct QeScratch {
     _Float16 *xhl;                          // [T][2048] normed x as fp16 hi|lo halves (store_hilo16 layout)
     float *logits;                          // [T][257]
     float *shgu;                            // prefill: shared silu(g)*u as [T][512] fp16 hi|lo halves
-    float *rpart;                           // [4][T][257] router subtree partials
+    float *rpart;                           // [8][T][256] router subtree partials
     int32_t *ids; float *wts; float *shg;   // [T][8], [T][8], [T]
     int32_t *off; int32_t *pairs;           // [257], [T*8]
     int4 *items; int32_t *n_items;          // work items (expert, first pair, count)

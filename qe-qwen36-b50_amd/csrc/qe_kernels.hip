@@ -3,9 +3,9 @@
 // Launch plans (host side in qe_api.hip):
 //  * small T (<= QE_SMALL_T tokens): the persistent kernel in qe_decode.hip;
 //  * large T (prefill, Engine::moe_batched, engine/qe.cpp:1957-2047):
-//      k_normq, k_router_split + k_router_combine, the shared-expert MFMA
-//      GEMMs and the routed-expert MFMA grouped GEMMs of qe_prefill.hip,
-//      k_topk, k_disp_hist, k_disp_scatter, k_combine.
+//      k_normq, k_router_split, the shared-expert MFMA GEMMs and the
+//      routed-expert MFMA grouped GEMMs of qe_prefill.hip, k_topk,
+//      k_disp_hist, k_disp_scatter, k_combine.
 // Routing (RMSNorm, router dot products, top-8) follows the checker's
 // canonical fp32 order exactly; expert products use exact int8 block dots
 // with fp32 block scaling, so they agree with the CPU path to fp32 rounding.
@@ -29,52 +29,52 @@ __global__ __launch_bounds__(256) void k_normq(const float *x, int T, const floa
     lane_quant_store_opnd(v, xqp + (size_t)t * QE_D, lane, xs + (size_t)t * (QE_D / 32) + lane);
 }
 
-// Router logits in the canonical fp32 order, tiled: C[m][n] = sum_k xn[m][k] W[n][k].
-// Canonical order: per 32-wide k chunk an fma chain from 0, chunk sums merged by
-// the pairwise tree (chunks (c, c+1), then pairs of pairs, ...).  The K range is
-// split four ways along that tree: split z computes the 16-chunk subtree
-// [16z, 16z+16) exactly, and k_router_combine forms (s0 + s1) + (s2 + s3), the
-// tree's top two levels -- bit-identical to the unsplit order, with 4x the
-// workgroups.  Tile 64 x 64, 256 threads, 4 x 4 outputs per thread.
+// Router logits 0..255 in the canonical fp32 order, tiled:
+// C[m][n] = sum_k xn[m][k] W[n][k].  Canonical order: per 32-wide k chunk an fma
+// chain from 0, chunk sums merged by the pairwise tree (chunks (c, c+1), then
+// pairs of pairs, ...).  The K range is split eight ways along that tree: split
+// z computes the 8-chunk subtree [8z, 8z+8) exactly, and k_topk forms the top
+// three levels ((s0 + s1) + (s2 + s3)) + ((s4 + s5) + (s6 + s7)) -- bit-identical
+// to the unsplit order.  Row 256 (the shared-expert gate) is one canonical wave
+// dot per token in k_topk.  Tile 64 tokens x 64 rows, 256 threads, 4 x 4 outputs
+// per thread; chunks are double-buffered in LDS, the next one loaded into
+// registers while the current one is multiplied.
+#define RT_SPLIT 8
 __global__ __launch_bounds__(256) void k_router_split(const float *xn, int T, const float *W, float *part) {
-    constexpr int NCH = 16; // chunks per split
-    __shared__ float As[32][68];
-    __shared__ float Bs[32][68];
+    constexpr int NCH = 64 / RT_SPLIT; // chunks per split
+    __shared__ float As[2][32][68];
+    __shared__ float Bs[2][32][68];
     const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
     const int m0 = blockIdx.y * 64, n0 = blockIdx.x * 64, z = blockIdx.z;
     const int lr = tid >> 2, lk = (tid & 3) * 8; // loader: row lr of the tile, 8 k values
-    float st[5][4][4];
+    const bool a_ok = m0 + lr < T;
+    const float *ap = xn + (size_t)(a_ok ? m0 + lr : 0) * QE_D + z * NCH * 32 + lk;
+    const float *bp = W + (size_t)(n0 + lr) * QE_D + z * NCH * 32 + lk;
+    float4 pa[2], pb[2];
+    auto fetch = [&](int cl) {
+        const float4 *a4 = (const float4 *)(ap + cl * 32), *b4 = (const float4 *)(bp + cl * 32);
+        pa[0] = a_ok ? a4[0] : make_float4(0.f, 0.f, 0.f, 0.f);
+        pa[1] = a_ok ? a4[1] : make_float4(0.f, 0.f, 0.f, 0.f);
+        pb[0] = b4[0];
+        pb[1] = b4[1];
+    };
+    auto stage = [&](int buf) {
+        const float va[8] = {pa[0].x, pa[0].y, pa[0].z, pa[0].w, pa[1].x, pa[1].y, pa[1].z, pa[1].w};
+        const float vb[8] = {pb[0].x, pb[0].y, pb[0].z, pb[0].w, pb[1].x, pb[1].y, pb[1].z, pb[1].w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            As[buf][lk + i][lr] = va[i];
+            Bs[buf][lk + i][lr] = vb[i];
+        }
+    };
+    fetch(0);
+    stage(0);
+    __syncthreads();
+    float st[4][4][4];
+#pragma unroll 1
     for (int cl = 0; cl < NCH; ++cl) {
-        const int c = z * NCH + cl;
-        {
-            const int m = m0 + lr;
-            float v[8];
-            if (m < T) {
-                const float4 *p = (const float4 *)(xn + (size_t)m * QE_D + c * 32 + lk);
-                const float4 p0 = p[0], p1 = p[1];
-                v[0] = p0.x; v[1] = p0.y; v[2] = p0.z; v[3] = p0.w; v[4] = p1.x; v[5] = p1.y; v[6] = p1.z; v[7] = p1.w;
-            } else {
-#pragma unroll
-                for (int i = 0; i < 8; ++i) v[i] = 0.f;
-            }
-#pragma unroll
-            for (int i = 0; i < 8; ++i) As[lk + i][lr] = v[i];
-        }
-        {
-            const int n = n0 + lr;
-            float v[8];
-            if (n < QE_ROUTER_ROWS) {
-                const float4 *p = (const float4 *)(W + (size_t)n * QE_D + c * 32 + lk);
-                const float4 p0 = p[0], p1 = p[1];
-                v[0] = p0.x; v[1] = p0.y; v[2] = p0.z; v[3] = p0.w; v[4] = p1.x; v[5] = p1.y; v[6] = p1.z; v[7] = p1.w;
-            } else {
-#pragma unroll
-                for (int i = 0; i < 8; ++i) v[i] = 0.f;
-            }
-#pragma unroll
-            for (int i = 0; i < 8; ++i) Bs[lk + i][lr] = v[i];
-        }
-        __syncthreads();
+        const int buf = cl & 1;
+        if (cl + 1 < NCH) fetch(cl + 1);
         float acc[4][4];
 #pragma unroll
         for (int i = 0; i < 4; ++i)
@@ -82,18 +82,17 @@ __global__ __launch_bounds__(256) void k_router_split(const float *xn, int T, co
             for (int j = 0; j < 4; ++j) acc[i][j] = 0.f;
 #pragma unroll
         for (int kk = 0; kk < 32; ++kk) {
-            const float4 av = *(const float4 *)&As[kk][ty * 4];
-            const float4 bv = *(const float4 *)&Bs[kk][tx * 4];
+            const float4 av = *(const float4 *)&As[buf][kk][ty * 4];
+            const float4 bv = *(const float4 *)&Bs[buf][kk][tx * 4];
             const float ar[4] = {av.x, av.y, av.z, av.w}, br[4] = {bv.x, bv.y, bv.z, bv.w};
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
                 for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(ar[i], br[j], acc[i][j]);
         }
-        __syncthreads();
         bool carry = true; // pairwise-tree merge of chunk cl
 #pragma unroll
-        for (int l = 0; l < 5; ++l) {
+        for (int l = 0; l < 4; ++l) {
             if (carry) {
                 if (cl & (1 << l)) {
 #pragma unroll
@@ -109,32 +108,55 @@ __global__ __launch_bounds__(256) void k_router_split(const float *xn, int T, co
                 }
             }
         }
+        if (cl + 1 < NCH) stage(buf ^ 1);
+        __syncthreads();
     }
+    constexpr int TOP = NCH == 8 ? 3 : NCH == 16 ? 4 : 2;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int m = m0 + ty * 4 + i;
         if (m >= T) continue;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int n = n0 + tx * 4 + j;
-            if (n < QE_ROUTER_ROWS) part[((size_t)z * T + m) * QE_ROUTER_ROWS + n] = st[4][i][j];
-        }
+        *(float4 *)&part[((size_t)z * T + m) * QE_N_EXPERT + n0 + tx * 4] =
+            make_float4(st[TOP][i][0], st[TOP][i][1], st[TOP][i][2], st[TOP][i][3]);
     }
 }
+static_assert(RT_SPLIT == 8, "k_topk merges eight router partials");
 
-__global__ __launch_bounds__(256) void k_router_combine(const float *part, int T, const float *bias, float *logits) {
-    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x, n = (size_t)T * QE_ROUTER_ROWS;
-    if (i >= n) return;
-    const int e = (int)(i % QE_ROUTER_ROWS);
-    float v = (part[i] + part[n + i]) + (part[2 * n + i] + part[3 * n + i]);
-    if (bias && e < QE_N_EXPERT) v = v + bias[e];
-    logits[i] = v;
-}
-
-__global__ __launch_bounds__(256) void k_topk(const float *logits, int T, int32_t *ids, float *wts, float *shg) {
+// Wave per token: logits (router partials merged + bias; row 256 as a canonical
+// wave dot), then top-8, weights and the shared gate (engine/qe.cpp:1454-1483).
+__global__ __launch_bounds__(256) void k_topk(const float *part, const float *xn, const float *W, const float *bias,
+                                              int T, float *logits, int32_t *ids, float *wts, float *shg) {
     const int lane = threadIdx.x & 63, t = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (t >= T) return;
-    wave_topk(logits + (size_t)t * QE_ROUTER_ROWS, lane, ids + t * QE_K_USED, wts + t * QE_K_USED, shg + t);
+    const size_t n = (size_t)T * QE_N_EXPERT;
+    float v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int e = lane + 64 * j;
+        const float *p = part + (size_t)t * QE_N_EXPERT + e;
+        float s[8];
+#pragma unroll
+        for (int z = 0; z < 8; ++z) s[z] = p[z * n];
+        float x = ((s[0] + s[1]) + (s[2] + s[3])) + ((s[4] + s[5]) + (s[6] + s[7]));
+        if (bias) x = x + bias[e];
+        v[j] = x;
+        logits[(size_t)t * QE_ROUTER_ROWS + e] = x;
+    }
+    float xv[32];
+    load32(xn + (size_t)t * QE_D + lane * 32, xv);
+    const float4 *w4 = (const float4 *)(W + (size_t)QE_N_EXPERT * QE_D + lane * 32);
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float4 w = w4[i];
+        acc = fmaf(xv[4 * i], w.x, acc);
+        acc = fmaf(xv[4 * i + 1], w.y, acc);
+        acc = fmaf(xv[4 * i + 2], w.z, acc);
+        acc = fmaf(xv[4 * i + 3], w.w, acc);
+    }
+    const float lg = wave_sum_canon(acc);
+    if (lane == 0) logits[(size_t)t * QE_ROUTER_ROWS + QE_N_EXPERT] = lg;
+    wave_topk_vals(v, lg, lane, ids + t * QE_K_USED, wts + t * QE_K_USED, shg + t);
 }
 
 // Dispatch pass 1: per-chunk (1024 pairs) expert histogram.
@@ -279,9 +301,7 @@ hipError_t qe_launch_layer(const QeLayerPtrs &L, const QeScratch &S, const float
     }
     {
         QE_PROF(QP_ROUTER);
-        k_router_split<<<dim3((QE_ROUTER_ROWS + 63) / 64, mt, 4), 256, 0, st>>>(S.xn, T, L.router, S.rpart);
-        k_router_combine<<<(unsigned)(((size_t)T * QE_ROUTER_ROWS + 255) / 256), 256, 0, st>>>(S.rpart, T, L.bias,
-                                                                                            S.logits);
+        k_router_split<<<dim3(QE_N_EXPERT / 64, mt, RT_SPLIT), 256, 0, st>>>(S.xn, T, L.router, S.rpart);
     }
     {
         QE_PROF(QP_SHGU);
@@ -289,7 +309,7 @@ hipError_t qe_launch_layer(const QeLayerPtrs &L, const QeScratch &S, const float
     }
     {
         QE_PROF(QP_TOPK);
-        k_topk<<<(T + 3) / 4, 256, 0, st>>>(S.logits, T, S.ids, S.wts, S.shg);
+        k_topk<<<(T + 3) / 4, 256, 0, st>>>(S.rpart, S.xn, L.router, L.bias, T, S.logits, S.ids, S.wts, S.shg);
     }
     {
         QE_PROF(QP_DISPATCH);
