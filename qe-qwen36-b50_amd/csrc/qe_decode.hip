@@ -17,18 +17,21 @@
 // Every value crossing workgroups is one 64-bit agent-scope store {value, tag}
 // with tag = (launch epoch, layer, stage), so a reader verifies what it reads.
 // Agent-scope relaxed atomics compile to sc1 accesses, coherent across the
-// XCDs' separate L2s without write-back fences.  The logits and the shared
-// activations are polled directly; the all-gathers of x and h first wait on
-// stage counters (groups of 16 workgroups) and then read their data once.
-// Every exchanged buffer and counter exists in REP copies: producers write
-// all of them, a workgroup reads copy blockIdx % REP, so ~32 workgroups poll
-// any one cache line instead of all 256 (the shared lines otherwise queue
-// the polls at their memory channel: ~5 us per exchange against a 0.6 us
-// one-way store->load latency measured between two workgroups).
-// Buffer reuse is ordered by the data flow: a workgroup writes a stage's
-// buffer for layer l+1 only after a wait that proves every workgroup has
-// finished reading it for layer l.  Weights a stage needs that do not depend
-// on the data being waited for are loaded before the wait.
+// XCDs' separate L2s without write-back fences.  Consumers poll the data
+// itself: the logits and shared activations word by word; for the all-gathers
+// of x and h, one word per producer first (the last it writes), then all of it
+// once with the tags verified (a word not there yet is re-read).
+// Every exchanged buffer exists in REP copies: producers write all of them, a
+// workgroup reads copy blockIdx % REP, so ~32 workgroups poll any one cache
+// line instead of all 256 (the shared lines otherwise queue the polls at
+// their memory channel: ~5 us per exchange against a 0.6 us one-way
+// store->load latency measured between two workgroups).
+// Buffer reuse needs no counters; the data flow orders it.  A workgroup
+// rewrites a buffer for layer l+1 only after reading all of x of layer l, and
+// every workgroup wrote its rows of x after its reads of layer l's logits, h
+// and shared activations, which those rows depend on (x itself alternates
+// between two buffers).  Weights a stage needs that do not depend on the data
+// being waited for are loaded before the wait.
 #include "qe_kernels.h"
 
 #define LD_A(p) __hip_atomic_load((p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
@@ -41,28 +44,32 @@
 #define DEC_PFI 16        /* items whose down rows are prefetched into registers during G */
 #define SYNC_EPOCH 0
 #define SYNC_EXIT 32
-#define SYNC_CTR 64       /* per replica: 3 stages x 16 groups, 32 words apart: (unused), G, D */
 #define REP QE_DEC_REP      /* copies of every exchanged buffer and counter */
-#define CTR_REP (3 * 16 * 32)
 #define SPIN_CAP (1 << 22)
 #define DEC_MIN_GRID 64   /* D row groups per workgroup stay <= 4 */
 #define N_RTASK (QE_ROUTER_ROWS + QE_FF_SH) /* router rows, then shared (gate, up) row pairs */
 
-// LDS layout (bytes)
+// LDS layout (bytes).  Rows read one 32-element chunk per lane are padded to
+// 33 words per chunk (or stored chunk-transposed) so a wave's reads hit 64
+// distinct banks instead of one.
+#define DEC_XSTR (QE_D + 32)                        /* floats per token in s_xn */
+QE_DEV int xpos(int e) { return (e & 31) * 65 + (e >> 5); } // raw x element e of a token in s_xn
 #define L_U 0                                       // union, by stage:
-#define L_XN L_U                                    //   R: f32 [T][32][64] xn, element-interleaved (raw x first)
+#define L_XN L_U                                    //   R: f32 [T][DEC_XSTR]: raw x at xpos(e), then xn at
+                                                    //      32 i + l -> i * 64 + l (lane l's chunk, transposed)
 #define L_GU L_U                                    //   G: f32 [64 rows][8 pairs] gate/up dots of a unit
-#define L_HF L_U                                    //   D: f32 [8][512] fp32 h (T = 1)
-#define L_HQ (L_U + 8 * QE_FF_EXP * 4)              //   D: int8 [T*8][512] quantised h
+#define L_HF L_U                                    //   D: f32 [8 x 16 blocks][33] fp32 h (T = 1), padded
+#define L_HQ (L_U + 8 * 16 * 33 * 4)                //   D: int8 [T*8][512] quantised h
 #define L_HS (L_HQ + DEC_T * 8 * QE_FF_EXP)         //   D: f32 [T*8][16] its block scales
 #define L_Y (L_HS + DEC_T * 8 * 16 * 4)             //   D: f32 [8 rows][2 halves][T] partials, [8][T] sd
-#define L_U_END (L_U + DEC_T * QE_D * 4)
+#define L_U_END (L_U + DEC_T * DEC_XSTR * 4)
 #define L_XQ L_U_END                                // int8 [T][2048]   quantised xn
 #define L_XS (L_XQ + DEC_T * QE_D)                  // f32 [T][64]      its block scales
 #define L_HSH (L_XS + DEC_T * 64 * 4)               // f32 [T][512]     shared-expert silu(g)*u
 #define L_RES (L_HSH + DEC_T * QE_FF_SH * 4)        // f32 [T][32]      raw x of this workgroup's D rows
 #define L_RW (L_RES + DEC_T * 32 * 4)               // [4 waves][8 KB] prefetched weights of the first row task
-#define L_ITEMS (L_RW + 4 * 8192)                   // int4 [64]
+#define L_PN (L_RW + 4 * 8192)                      // f32 [32][65] post_norm, element e at (e / 64) * 65 + e % 64
+#define L_ITEMS (L_PN + 32 * 65 * 4)                // int4 [64]
 #define L_PAIRS (L_ITEMS + 64 * 16)                 // int [64]
 #define L_IDS (L_PAIRS + 64 * 4)                    // int [64]
 #define L_WTS (L_IDS + 64 * 4)                      // f32 [64]
@@ -81,7 +88,7 @@ static_assert(L_TOTAL <= 160 * 1024, "LDS budget of one workgroup per CU");
 #define EX_HF (EX_HQ + DEC_T * 8 * 16 * 9)          // [8][512] f32 h (T = 1)
 #define EX_TOTAL (EX_HF + 8 * QE_FF_EXP)           // one replica
 static_assert(REP * EX_TOTAL == QE_DECODE_EX_WORDS, "exchange size must match the allocation");
-static_assert(SYNC_CTR + REP * CTR_REP <= QE_DECODE_SYNC_WORDS, "sync words must match the allocation");
+static_assert(SYNC_EXIT < QE_DECODE_SYNC_WORDS, "sync words must match the allocation");
 
 QE_DEV uint64_t pack_tv(float v, unsigned tag) { return ((uint64_t)tag << 32) | __float_as_uint(v); }
 QE_DEV float tv_val(uint64_t w) { return __uint_as_float((unsigned)w); }
@@ -145,97 +152,6 @@ QE_DEV void poll_tv2(const uint64_t *src, int stride, unsigned tag, uint64_t w[N
     }
 }
 
-// Stage counters: after issuing all of its tagged data stores a workgroup
-// bumps its group's counter for the stage (groups of 16 workgroups; the add
-// is posted, nothing waits on it).  A consumer's wave 0 polls the <= 16 group
-// counters of the stage until each reaches 16 * round, then every thread
-// reads its data once (tags verified, rare retry).  Measured on MI355X with
-// 256 workgroups: ~4.2 us per all-gather this way, against ~5.5 us polling
-// one flag per workgroup and ~5.7 us polling the data itself.
-QE_DEV void stage_arrive(unsigned *ctr) { // ctr: replica 0 of the stage
-    __syncthreads();
-    if (threadIdx.x < REP) (void)ADD_A(ctr + threadIdx.x * CTR_REP + (blockIdx.x >> 4) * 32, 1u);
-}
-// The poll keeps four loads in flight, spaced by a short sleep, so a count
-// that lands is seen ~1/4 of a memory round trip later rather than up to one.
-QE_DEV void stage_wait(const unsigned *ctr, unsigned round, unsigned *err) {
-    if (threadIdx.x < 64) {
-        const int g = threadIdx.x, ng = (gridDim.x + 15) >> 4;
-        const unsigned gsz = (unsigned)((g + 1) * 16 <= (int)gridDim.x ? 16 : (int)gridDim.x - g * 16);
-        const unsigned want = g < ng ? gsz * round : 0u;
-        unsigned *p = (unsigned *)ctr + (blockIdx.x % REP) * CTR_REP + (g < ng ? g : 0) * 32;
-        unsigned v[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            v[i] = LD_A(p);
-            __builtin_amdgcn_s_sleep(2);
-        }
-        for (int spins = 0;; spins += 4) {
-            bool done = false;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                if (__all(v[i] >= want)) { done = true; break; }
-                v[i] = LD_A(p);
-                __builtin_amdgcn_s_sleep(2);
-            }
-            if (done) break;
-            if (spins > SPIN_CAP) { ST_A(err, 1u); break; }
-        }
-    }
-    __syncthreads();
-}
-
-// Order-preserving u32 image of a float (-0 folded onto +0 by the caller).
-QE_DEV unsigned f2ord(float v) {
-    const unsigned u = __float_as_uint(v);
-    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
-QE_DEV float ord2f(unsigned o) { return __uint_as_float((o & 0x80000000u) ? (o & 0x7fffffffu) : ~o); }
-
-// top-8 of 256 logits held as v[j] = logit(lane + 64 j), the engine/qe.cpp:1454-1483
-// order: larger value first, ties to the smaller (e % 16, e / 16).  Each candidate
-// is one u64 {ordered value, 0xffff - key} so a wave max finds value and key together.
-QE_DEV void wave_topk8(float v[4], float lg_sh, int lane, int *ids, float *wts, float *shg) {
-    uint64_t c[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int e = lane + 64 * j, key = (e & 15) * 16 + (e >> 4);
-        c[j] = ((uint64_t)f2ord(v[j] + 0.0f) << 32) | (unsigned)(0xffff - key);
-    }
-    float sel[QE_K_USED];
-    int id[QE_K_USED];
-#pragma unroll
-    for (int k = 0; k < QE_K_USED; ++k) {
-        uint64_t b = c[0];
-#pragma unroll
-        for (int j = 1; j < 4; ++j) b = c[j] > b ? c[j] : b;
-#pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-            const uint64_t o = ((uint64_t)(unsigned)__shfl_xor((int)(b >> 32), off, 64) << 32) |
-                               (unsigned)__shfl_xor((int)(unsigned)b, off, 64);
-            b = o > b ? o : b;
-        }
-        const int key = 0xffff - (int)(b & 0xffff);
-        const int e = (key & 15) * 16 + (key >> 4);
-        sel[k] = ord2f((unsigned)(b >> 32));
-        id[k] = e;
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-            if (c[j] == b) c[j] = 0;
-    }
-    if (lane == 0) {
-        float s = 0.f;
-#pragma unroll
-        for (int k = 0; k < QE_K_USED; ++k) s += expf(sel[k] - sel[0]);
-#pragma unroll
-        for (int k = 0; k < QE_K_USED; ++k) {
-            ids[k] = id[k];
-            wts[k] = expf(sel[k] - sel[0]) / s;
-        }
-        *shg = 1.f / (1.f + expf(-lg_sh));
-    }
-}
-
 // Gate/up rows of one unit: this lane's NB blocks of its row (blocks c + LPR i,
 // LPR = 64 / NB lanes per row), dotted with the int8 x of every pair of the item;
 // the row total lands in s_gu[row_in_unit * 8 + pair].
@@ -269,8 +185,10 @@ QE_DEV void unit_rows(const uint8_t *row, int c, int row_in_unit, const int4 it,
             const uint4 x0 = *(const uint4 *)(xq + b * 32), x1 = *(const uint4 *)(xq + b * 32 + 16);
             acc = fmaf(dw[i] * xs[b], (float)nl4_block_dot(w, x0, x1), acc);
         }
-#pragma unroll
-        for (int off = 1; off < LPR; off <<= 1) acc = acc + __shfl_xor(acc, off, 64);
+        static_assert(LPR == 16 || LPR == 32 || LPR == 64, "row reduction over 16, 32 or 64 lanes");
+        acc = sum16(acc);
+        if (LPR >= 32) acc = add_rows16(acc);
+        if (LPR == 64) acc = add_rows32(acc);
         if (c == 0) s_gu[row_in_unit * 8 + jp] = acc;
     }
 }
@@ -280,6 +198,7 @@ template <int TM>
 __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
     extern __shared__ __align__(16) uint8_t lds[];
     float *s_xn = (float *)(lds + L_XN);
+    float *s_pn = (float *)(lds + L_PN);
     float *s_gu = (float *)(lds + L_GU);
     float *s_hf = (float *)(lds + L_HF);
     int8_t *s_hq = (int8_t *)(lds + L_HQ);
@@ -303,7 +222,6 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
     const unsigned epoch = (unsigned)s_misc[1];
     uint64_t *EX = a.ex;                                   // replica 0 (writes go to all REP)
     const uint64_t *EXr = a.ex + (size_t)(blockIdx.x % REP) * EX_TOTAL; // the copy this workgroup reads
-    unsigned *CG = a.sync + SYNC_CTR + 16 * 32, *CD = CG + 16 * 32;
     constexpr bool mode16 = TM == 1; // 16-row units, fp32 h (one token: 8 items x 32 units fill the grid)
     const int rb0 = blockIdx.x * 8;
 
@@ -361,32 +279,53 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
                                                  (__attribute__((address_space(3))) void *)(rw_lds + 4096 + 256), 2, 0, 0);
             }
         }
-        if (li > 0) stage_wait(CD, (unsigned)li, a.err);
+        if (pnorm && wv == 4) { // post_norm -> LDS, 64-element rows padded to 65 words (one dword per lane)
+#pragma unroll
+            for (int i = 0; i < 32; ++i)
+                __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)(pnorm + i * 64 + lane),
+                                                 (__attribute__((address_space(3))) void *)(s_pn + i * 65), 4, 0, 0);
+        }
+        if (li > 0) { // x: one word per (8-row group, token) polled first, then all read with tags verified
+            if (tid < T * 256) {
+                uint64_t w[1];
+                poll_tv2<1>(src_x + (tid >> 8) * QE_D + (tid & 255) * 8 + 7, 0, tagIn, w, true, a.err);
+            }
+            __syncthreads();
+        }
         // raw x of all tokens -> LDS (natural layout, token stride 2048; T*2048 is a multiple of 2 NTH)
         if (li == 0) {
-            for (int i = tid; i < T * QE_D; i += NTH) s_xn[i] = a.x_in[i];
+            for (int i = tid; i < T * QE_D; i += NTH) s_xn[(i >> 11) * DEC_XSTR + xpos(i & 2047)] = a.x_in[i];
         } else {
             for (int i0 = 0; i0 < T * QE_D; i0 += 2 * NTH) {
                 uint64_t w[2];
                 read_tv<2>(src_x + i0 + tid, NTH, tagIn, w, true, a.err);
-                s_xn[i0 + tid] = tv_val(w[0]);
-                s_xn[i0 + tid + NTH] = tv_val(w[1]);
+                const int e0 = i0 + tid, e1 = e0 + NTH;
+                s_xn[(e0 >> 11) * DEC_XSTR + xpos(e0 & 2047)] = tv_val(w[0]);
+                s_xn[(e1 >> 11) * DEC_XSTR + xpos(e1 & 2047)] = tv_val(w[1]);
             }
         }
         __syncthreads();
-        if (a.residual && tid < T * 8 * d_iters) { // raw x of this workgroup's D rows
-            const int t = tid / (8 * d_iters), k = tid % (8 * d_iters), m = k >> 3;
-            const int r = (blockIdx.x + m * gridDim.x) * 8 + (k & 7);
-            s_res[t * 32 + k] = r < QE_D ? s_xn[t * QE_D + r] : 0.f;
-        }
-        if (wv < T) { // wave t: norm + quantise token t; lane = 32-element chunk (reads precede writes in LDS order)
+        if (wv < T) { // wave t: token t's residual rows, then its norm + quantisation, in place
             const int t = wv;
-            float v[32];
+            float *xt = s_xn + t * DEC_XSTR;
+            if (a.residual && lane < 8 * d_iters) { // raw x of this workgroup's D rows
+                const int r = (blockIdx.x + (lane >> 3) * gridDim.x) * 8 + (lane & 7);
+                s_res[t * 32 + lane] = r < QE_D ? xt[xpos(r)] : 0.f;
+            }
+            float v[32]; // lane = 32-element chunk
 #pragma unroll
-            for (int i = 0; i < 32; ++i) v[i] = s_xn[t * QE_D + lane * 32 + i];
-            wave_norm_chunk(v, pnorm, lane);
+            for (int i = 0; i < 32; ++i) v[i] = xt[i * 65 + lane];
+            if (pnorm) { // wave_norm_chunk with the weights from LDS
+                float ss = 0.f;
 #pragma unroll
-            for (int i = 0; i < 32; ++i) s_xn[t * QE_D + i * 64 + lane] = v[i];
+                for (int i = 0; i < 32; ++i) ss = fmaf(v[i], v[i], ss);
+                ss = wave_sum_canon(ss);
+                const float inv = 1.0f / sqrtf(ss / (float)QE_D + QE_RMS_EPS);
+#pragma unroll
+                for (int i = 0; i < 32; ++i) v[i] = (v[i] * inv) * s_pn[(lane >> 1) * 65 + (lane & 1) * 32 + i];
+            }
+#pragma unroll
+            for (int i = 0; i < 32; ++i) xt[i * 64 + lane] = v[i]; // all reads of the wave precede
             lane_quant_store(v, s_xq + t * QE_D + lane * 32, s_xs + t * 64 + lane);
             if (last && blockIdx.x == 0 && a.xn_out) {
 #pragma unroll
@@ -409,7 +348,7 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
                 for (int t = 0; t < T; ++t) {
                     float acc = 0.f;
 #pragma unroll
-                    for (int i = 0; i < 32; ++i) acc = fmaf(wr[i], s_xn[t * QE_D + i * 64 + lane], acc);
+                    for (int i = 0; i < 32; ++i) acc = fmaf(wr[i], s_xn[t * DEC_XSTR + i * 64 + lane], acc);
                     acc = wave_sum_canon(acc);
                     if (lane < REP) ST_A(EX + lane * EX_TOTAL + EX_L + t * QE_ROUTER_ROWS + task, pack_tv(add_bias ? acc + b : acc, tagR));
                 }
@@ -440,7 +379,7 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
                     float ag = 0.f, au = 0.f;
 #pragma unroll
                     for (int i = 0; i < 32; ++i) {
-                        const float xv = s_xn[t * QE_D + i * 64 + lane];
+                        const float xv = s_xn[t * DEC_XSTR + i * 64 + lane];
                         ag = fmaf(wg[i], xv, ag);
                         au = fmaf(wu[i], xv, au);
                     }
@@ -466,7 +405,7 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
                 for (int j = 0; j < 4; ++j) a.logits[t * QE_ROUTER_ROWS + lane + 64 * j] = v[j];
                 if (lane == 0) a.logits[t * QE_ROUTER_ROWS + QE_N_EXPERT] = v[4];
             }
-            wave_topk8(v, v[4], lane, s_ids + t * QE_K_USED, s_wts + t * QE_K_USED, s_shg + t);
+            wave_topk_vals(v, v[4], lane, s_ids + t * QE_K_USED, s_wts + t * QE_K_USED, s_shg + t);
         }
         __syncthreads();
         if (wv == 0) {
@@ -571,8 +510,7 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
                 const int jp = tid >> 5, r = tid & 31;
                 const float hv = silu_mul(s_gu[r * 8 + jp], s_gu[(32 + r) * 8 + jp]);
                 float amax = fabsf(hv);
-#pragma unroll
-                for (int off = 1; off < 32; off <<= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+                amax = max32(amax);
                 float d;
                 const float id = quant_scale_inv(amax, d);
                 const unsigned qv = (unsigned)(uint8_t)quant_one(hv, id);
@@ -588,29 +526,35 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
             __syncthreads(); // s_gu is reused by the next unit
         }
         d_prefetch(); // workgroups without a unit
-        stage_arrive(CG);
 
         // ================= D: routed down + shared down + combine =================
-        stage_wait(CG, (unsigned)li + 1u, a.err);
+        // No counter: h is polled through its tags.  For T = 1 one word per unit
+        // (its last row) is polled first, then everything is read with the tags
+        // verified (a late word is re-read).
+        if (mode16 && tid < 256) {
+            uint64_t w[1];
+            poll_tv2<1>(EXr + EX_HF + (tid >> 5) * QE_FF_EXP + (tid & 31) * 16 + 15, 0, tagG, w, true, a.err);
+        }
         // shared-expert activations of every token: written in R, long landed by now
-        // (every workgroup has passed G); read once, tags verified
         for (int i = tid; i < T * QE_FF_SH; i += NTH) {
             uint64_t w[1];
             read_tv<1>(EXr + EX_HSH + i, 0, tagR, w, true, a.err);
             s_hsh[i] = tv_val(w[0]);
         }
         if (mode16) { // fp32 h of the 8 pairs -> LDS, then int8 per 32 rows
-            for (int i0 = 0; i0 < 8 * QE_FF_EXP; i0 += 2 * NTH) {
-                uint64_t w[2];
-                read_tv<2>(EXr + EX_HF + i0 + tid, NTH, tagG, w, true, a.err);
-                s_hf[i0 + tid] = tv_val(w[0]);
-                s_hf[i0 + tid + NTH] = tv_val(w[1]);
+            static_assert(8 * QE_FF_EXP == 4 * NTH, "h of the 8 pairs: four words per thread");
+            uint64_t w[4];
+            read_tv<4>(EXr + EX_HF + tid, NTH, tagG, w, true, a.err);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) { // (pair, block) rows of 33 floats
+                const int e = tid + i * NTH;
+                s_hf[(e >> 5) * 33 + (e & 31)] = tv_val(w[i]);
             }
             __syncthreads();
             if (tid < 8 * 16) { // thread (pair, block)
                 float v[32];
 #pragma unroll
-                for (int i = 0; i < 32; ++i) v[i] = s_hf[tid * 32 + i];
+                for (int i = 0; i < 32; ++i) v[i] = s_hf[tid * 33 + i];
                 lane_quant_store(v, s_hq + tid * 32, s_hs + tid);
             }
         } else {
@@ -662,8 +606,7 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
             }
 #pragma unroll
             for (int t = 0; t < TM; ++t) {
-                y[t] = y[t] + __shfl_xor(y[t], 16, 64);
-                y[t] = y[t] + __shfl_xor(y[t], 32, 64);
+                y[t] = add_rows32(add_rows16(y[t]));
             }
             if (lane == 0) {
 #pragma unroll
@@ -709,16 +652,13 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
             }
             __syncthreads(); // s_y is rewritten by the next row group
         }
-        if (!last) stage_arrive(CD);
         __syncthreads(); // the LDS union is rewritten by the next layer's R stage
     }
 
-    // the last workgroup out clears the stage counters and advances the epoch,
-    // so the next launch starts from zero counts with new tags
+    // the last workgroup out advances the epoch, so the next launch uses new tags
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (threadIdx.x == 0 && ADD_A(a.sync + SYNC_EXIT, 1u) == gridDim.x - 1) {
-        for (int i = 0; i < REP * 3 * 16; ++i) ST_A(a.sync + SYNC_CTR + i * 32, 0u);
         ST_A(a.sync + SYNC_EXIT, 0u);
         ST_A(a.sync + SYNC_EPOCH, epoch + 1u);
     }
@@ -734,8 +674,8 @@ template <int TM> static hipError_t launch_decode(const QeDecodeArgs &a, hipStre
         if ((e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev)) != hipSuccess) return e;
         if ((e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_decode<TM>, NTH, L_TOTAL)) != hipSuccess) return e;
         if (per_cu < 1) return hipErrorInvalidConfiguration;
-        // one workgroup per CU, 64..256 of them (stage counters cover 16 groups of 16; a
-        // workgroup's D rows, <= 4 groups of 8, stay within the 32-row residual buffer)
+        // one workgroup per CU, 64..256 of them (a workgroup's D rows, <= 4 groups
+        // of 8, stay within the 32-row residual buffer)
         grid = cus < 256 ? cus : 256;
         if (grid < DEC_MIN_GRID) return hipErrorInvalidConfiguration;
     }

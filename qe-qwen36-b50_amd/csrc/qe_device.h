@@ -59,24 +59,89 @@ QE_DEV float f16_bits_to_f32(uint16_t h) {
 // ---------------------------------------------------------------------------
 // cross-lane sums
 // ---------------------------------------------------------------------------
-// Canonical butterfly over 64 lanes (offsets 1,2,4,...,32): every lane ends
-// with the pairwise-tree sum of the 64 lane values, the order the CPU checker
-// restates for router rows and RMSNorm.
-QE_DEV float wave_sum_canon(float v) {
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) v = v + __shfl_xor(v, off, 64);
+// Lane exchanges are single VALU ops: DPP within 16-lane rows and the gfx950
+// row swaps across rows (an __shfl_xor is a ds_bpermute, an LDS round trip).
+//   QE_DPP_XOR1 / XOR2: quad_perm [1,0,3,2] / [2,3,0,1];
+//   QE_DPP_HMIRROR: lane i <-> 7 - i within 8;  QE_DPP_MIRROR: i <-> 15 - i within 16.
+// After a reduction over aligned groups of g lanes every lane of a group holds
+// the group's value, so a mirror pairs each lane with the other half's value
+// exactly as the xor butterfly would.
+#define QE_DPP_XOR1 0xB1
+#define QE_DPP_XOR2 0x4E
+#define QE_DPP_HMIRROR 0x141
+#define QE_DPP_MIRROR 0x140
+template <int CTRL> QE_DEV unsigned dpp_u(unsigned v) {
+    return (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xf, 0xf, false);
+}
+template <int CTRL> QE_DEV float dpp_f(float v) { return __uint_as_float(dpp_u<CTRL>(__float_as_uint(v))); }
+// Rows of 16 lanes r0..r3: a = [r0 r0 r2 r2], b = [r1 r1 r3 r3] (16-lane swap)
+// or a = [r0 r1 r0 r1], b = [r2 r3 r2 r3] (32-lane swap) of v.
+QE_DEV void rows16(unsigned v, unsigned &a, unsigned &b) {
+    const auto s = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    a = s[0];
+    b = s[1];
+}
+QE_DEV void rows32(unsigned v, unsigned &a, unsigned &b) {
+    const auto s = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    a = s[0];
+    b = s[1];
+}
+// Sum within aligned groups of 16 lanes, pairwise tree (lanes (i, i^1) first).
+QE_DEV float sum16(float v) {
+    v = v + dpp_f<QE_DPP_XOR1>(v);
+    v = v + dpp_f<QE_DPP_XOR2>(v);
+    v = v + dpp_f<QE_DPP_HMIRROR>(v);
+    v = v + dpp_f<QE_DPP_MIRROR>(v);
     return v;
 }
-// Sum within aligned groups of 16 lanes.
-QE_DEV float sum16(float v) {
-#pragma unroll
-    for (int off = 1; off < 16; off <<= 1) v = v + __shfl_xor(v, off, 64);
-    return v;
+// Rows of a 16-uniform value: [r0 + r1, r0 + r1, r2 + r3, r2 + r3] / sum of all four.
+QE_DEV float add_rows16(float v) {
+    unsigned a, b;
+    rows16(__float_as_uint(v), a, b);
+    return __uint_as_float(a) + __uint_as_float(b);
+}
+QE_DEV float add_rows32(float v) {
+    unsigned a, b;
+    rows32(__float_as_uint(v), a, b);
+    return __uint_as_float(a) + __uint_as_float(b);
+}
+// Canonical pairwise tree over 64 lanes (lane pairs, then pairs of pairs, ...):
+// every lane ends with the tree sum of the 64 lane values, the order the CPU
+// checker restates for router rows and RMSNorm.
+QE_DEV float wave_sum_canon(float v) { return add_rows32(add_rows16(sum16(v))); }
+QE_DEV float max16(float v) {
+    v = fmaxf(v, dpp_f<QE_DPP_XOR1>(v));
+    v = fmaxf(v, dpp_f<QE_DPP_XOR2>(v));
+    v = fmaxf(v, dpp_f<QE_DPP_HMIRROR>(v));
+    return fmaxf(v, dpp_f<QE_DPP_MIRROR>(v));
+}
+// maximum within aligned groups of 32 lanes
+QE_DEV float max32(float v) {
+    unsigned a, b;
+    rows16(__float_as_uint(max16(v)), a, b);
+    return fmaxf(__uint_as_float(a), __uint_as_float(b));
 }
 QE_DEV float wave_max(float v) {
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-    return v;
+    unsigned a, b;
+    rows32(__float_as_uint(max32(v)), a, b);
+    return fmaxf(__uint_as_float(a), __uint_as_float(b));
+}
+QE_DEV uint64_t umax64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+template <int CTRL> QE_DEV uint64_t dpp64(uint64_t v) {
+    return ((uint64_t)dpp_u<CTRL>((unsigned)(v >> 32)) << 32) | dpp_u<CTRL>((unsigned)v);
+}
+QE_DEV uint64_t wave_max_u64(uint64_t v) {
+    v = umax64(v, dpp64<QE_DPP_XOR1>(v));
+    v = umax64(v, dpp64<QE_DPP_XOR2>(v));
+    v = umax64(v, dpp64<QE_DPP_HMIRROR>(v));
+    v = umax64(v, dpp64<QE_DPP_MIRROR>(v));
+    unsigned al, bl, ah, bh;
+    rows16((unsigned)v, al, bl);
+    rows16((unsigned)(v >> 32), ah, bh);
+    v = umax64(((uint64_t)ah << 32) | al, ((uint64_t)bh << 32) | bl);
+    rows32((unsigned)v, al, bl);
+    rows32((unsigned)(v >> 32), ah, bh);
+    return umax64(((uint64_t)ah << 32) | al, ((uint64_t)bh << 32) | bl);
 }
 
 // ---------------------------------------------------------------------------
@@ -102,41 +167,54 @@ QE_DEV float silu_mul(float g, float u) { return g / (1.f + expf(-g)) * u; }
 // reference's 16-lane reduction produces.  Lane l holds e = l + 64 j.
 // ===========================================================================
 // v[j] = logit of expert lane + 64 j; lg_sh = logit 256 (shared-expert gate).
-QE_DEV void wave_topk_vals(float v[4], float lg_sh, int lane, int32_t *ids, float *wts, float *shg) {
+// Each round: one wave max of the values, then ballots of the lanes holding
+// it; a single holder wins, several (a tie) go to the smallest key
+// (e % 16) * 16 + e / 16.  -0 and +0 compare equal, as in the reference.
+// The softmax weights run one per lane; their sum keeps the reference's
+// order k = 0..7.
+QE_DEV void wave_topk_vals(const float v_in[4], float lg_sh, int lane, int32_t *ids, float *wts, float *shg) {
+    float v[4] = {v_in[0], v_in[1], v_in[2], v_in[3]};
     float sel[QE_K_USED];
     int id[QE_K_USED];
 #pragma unroll
     for (int k = 0; k < QE_K_USED; ++k) {
-        float bv = -INFINITY;
-        int bk = 1 << 20, be = 0;
+        const float m = wave_max(fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])));
+        uint64_t b[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int e = lane + 64 * j, key = (e & 15) * 16 + (e >> 4);
-            if (v[j] > bv || (v[j] == bv && key < bk)) { bv = v[j]; bk = key; be = e; }
+        for (int j = 0; j < 4; ++j) b[j] = __ballot(v[j] == m);
+        int e;
+        if (__popcll(b[0]) + __popcll(b[1]) + __popcll(b[2]) + __popcll(b[3]) == 1) {
+            const int j = b[0] ? 0 : b[1] ? 1 : b[2] ? 2 : 3;
+            e = 64 * j + __ffsll((long long)b[j]) - 1;
+        } else {
+            int bkey = 1 << 20;
+            e = 0;
+            for (int j = 0; j < 4; ++j)
+                for (uint64_t mk = b[j]; mk; mk &= mk - 1) {
+                    const int l = __ffsll((long long)mk) - 1, ee = 64 * j + l, key = (ee & 15) * 16 + (ee >> 4);
+                    if (key < bkey) { bkey = key; e = ee; }
+                }
         }
-#pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-            const float ov = __shfl_xor(bv, off, 64);
-            const int ok = __shfl_xor(bk, off, 64), oe = __shfl_xor(be, off, 64);
-            if (ov > bv || (ov == bv && ok < bk)) { bv = ov; bk = ok; be = oe; }
-        }
-        sel[k] = bv;
-        id[k] = be;
+        sel[k] = m;
+        id[k] = e;
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-            if (lane + 64 * j == be) v[j] = -INFINITY;
+            if (64 * j + lane == e) v[j] = -INFINITY;
     }
-    if (lane == 0) {
-        float s = 0.f;
+    float mine = sel[0];
+    int myid = id[0];
 #pragma unroll
-        for (int k = 0; k < QE_K_USED; ++k) s += expf(sel[k] - sel[0]);
+    for (int k = 1; k < QE_K_USED; ++k)
+        if (lane == k) { mine = sel[k]; myid = id[k]; }
+    const float ex = expf(mine - sel[0]);
+    float s = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ex), 0));
 #pragma unroll
-        for (int k = 0; k < QE_K_USED; ++k) {
-            ids[k] = id[k];
-            wts[k] = expf(sel[k] - sel[0]) / s;
-        }
-        *shg = 1.f / (1.f + expf(-lg_sh));
+    for (int k = 1; k < QE_K_USED; ++k) s += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ex), k));
+    if (lane < QE_K_USED) {
+        ids[lane] = myid;
+        wts[lane] = ex / s;
     }
+    if (lane == QE_K_USED) *shg = 1.f / (1.f + expf(-lg_sh));
 }
 QE_DEV void wave_topk(const float *lg, int lane, int32_t *ids, float *wts, float *shg) {
     float v[4];

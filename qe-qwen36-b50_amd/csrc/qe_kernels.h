@@ -82,7 +82,7 @@ struct QeDecodeArgs {
     uint64_t *ex;        // exchange words {value, tag}, QE_DECODE_EX_WORDS of them (qe_decode.hip)
     // routing sink of the last layer (plain stores by workgroup 0)
     float *logits; int32_t *ids; float *wts; float *shg; int32_t *off; int32_t *pairs; float *sd_out; float *xn_out;
-    unsigned *sync;      // QE_DECODE_SYNC_WORDS: [0] launch epoch, [32] exit counter, [64..) stage counters
+    unsigned *sync;      // QE_DECODE_SYNC_WORDS: [0] launch epoch, [32] exit counter
     unsigned *err;       // set to 1 if a poll timed out
 };
 hipError_t qe_launch_decode(const QeDecodeArgs &a, hipStream_t st);
@@ -91,7 +91,7 @@ hipError_t qe_launch_decode(const QeDecodeArgs &a, hipStream_t st);
 #endif
 #define QE_DECODE_EX_WORDS \
     (QE_DEC_REP * (2 * QE_SMALL_T * QE_D + QE_SMALL_T * QE_ROUTER_ROWS + QE_SMALL_T * QE_FF_SH + QE_SMALL_T * 8 * 16 * 9 + 8 * QE_FF_EXP))
-#define QE_DECODE_SYNC_WORDS (64 + QE_DEC_REP * 3 * 16 * 32) /* epoch, exit counter, stage counters 128 B apart */
+#define QE_DECODE_SYNC_WORDS 64 /* launch epoch, exit counter */
 
 // Launchers (qe_kernels.hip).  xin: layer input; post_norm: nullptr = input is
 // already normalised; x2: residual added to the output or nullptr.

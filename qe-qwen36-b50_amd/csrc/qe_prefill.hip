@@ -290,8 +290,7 @@ __device__ __forceinline__ void expert_tile(const GemmTileArgs &a, const int4 it
                 const float h0 = silu_mul(acc[0][t][i], acc[2][t][i]);
                 const float h1 = silu_mul(acc[1][t][i], acc[3][t][i]);
                 float m = fmaxf(fabsf(h0), fabsf(h1));
-#pragma unroll
-                for (int off = 1; off < 16; off <<= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+                m = max16(m);
                 float d;
                 const float id = quant_scale_inv(m, d);
                 const int p = s_pair[16 * t + 4 * g + i];
