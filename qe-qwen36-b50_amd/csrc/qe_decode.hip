@@ -55,11 +55,9 @@
 #define DEC_XSTR (QE_D + 32)                        /* floats per token in s_xn */
 QE_DEV int xpos(int e) { return (e & 31) * 65 + (e >> 5); } // raw x element e of a token in s_xn
 #define L_U 0                                       // union, by stage:
-#define L_XN L_U                                    //   R: f32 [T][DEC_XSTR]: raw x at xpos(e), then xn at
-                                                    //      32 i + l -> i * 64 + l (lane l's chunk, transposed)
+#define L_XN L_U                                    //   R: f32 [T][DEC_XSTR]: raw x, then xn, element e at xpos(e)
 #define L_GU L_U                                    //   G: f32 [64 rows][8 pairs] gate/up dots of a unit
-#define L_HF L_U                                    //   D: f32 [8 x 16 blocks][33] fp32 h (T = 1), padded
-#define L_HQ (L_U + 8 * 16 * 33 * 4)                //   D: int8 [T*8][512] quantised h
+#define L_HQ (L_U + 64 * 8 * 4)                     //   D: int8 [T*8][512] quantised h
 #define L_HS (L_HQ + DEC_T * 8 * QE_FF_EXP)         //   D: f32 [T*8][16] its block scales
 #define L_Y (L_HS + DEC_T * 8 * 16 * 4)             //   D: f32 [8 rows][2 halves][T] partials, [8][T] sd
 #define L_U_END (L_U + DEC_T * DEC_XSTR * 4)
@@ -75,7 +73,8 @@ QE_DEV int xpos(int e) { return (e & 31) * 65 + (e >> 5); } // raw x element e o
 #define L_WTS (L_IDS + 64 * 4)                      // f32 [64]
 #define L_SHG (L_WTS + 64 * 4)                      // f32 [8]
 #define L_MISC (L_SHG + 8 * 4)                      // int [16]
-#define L_TOTAL (L_MISC + 16 * 4)
+#define L_INV (L_MISC + 16 * 4)                     // f32 [8]          1 / rms of each token
+#define L_TOTAL (L_INV + 8 * 4)
 static_assert(L_Y + (8 * 2 * DEC_T + 8 * DEC_T) * 4 <= L_U_END, "D-stage LDS must fit in the union");
 static_assert(64 * 8 * 4 <= L_HQ - L_U, "G-stage LDS must fit in front of the D buffers");
 static_assert(L_TOTAL <= 160 * 1024, "LDS budget of one workgroup per CU");
@@ -199,8 +198,8 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
     extern __shared__ __align__(16) uint8_t lds[];
     float *s_xn = (float *)(lds + L_XN);
     float *s_pn = (float *)(lds + L_PN);
+    float *s_inv = (float *)(lds + L_INV);
     float *s_gu = (float *)(lds + L_GU);
-    float *s_hf = (float *)(lds + L_HF);
     int8_t *s_hq = (int8_t *)(lds + L_HQ);
     float *s_hs = (float *)(lds + L_HS);
     float *s_y = (float *)(lds + L_Y);
@@ -305,32 +304,46 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
             }
         }
         __syncthreads();
-        if (wv < T) { // wave t: token t's residual rows, then its norm + quantisation, in place
+        // RMSNorm (wave_norm_chunk's arithmetic, spread over the workgroup): wave t
+        // takes the residual rows of token t and its sum of squares in the
+        // canonical order (lane = 32-element chunk); then every thread scales,
+        // stores in place and quantises 2 elements per token (16 lanes per block).
+        if (wv < T) {
             const int t = wv;
-            float *xt = s_xn + t * DEC_XSTR;
+            const float *xt = s_xn + t * DEC_XSTR;
             if (a.residual && lane < 8 * d_iters) { // raw x of this workgroup's D rows
                 const int r = (blockIdx.x + (lane >> 3) * gridDim.x) * 8 + (lane & 7);
                 s_res[t * 32 + lane] = r < QE_D ? xt[xpos(r)] : 0.f;
             }
-            float v[32]; // lane = 32-element chunk
-#pragma unroll
-            for (int i = 0; i < 32; ++i) v[i] = xt[i * 65 + lane];
-            if (pnorm) { // wave_norm_chunk with the weights from LDS
+            if (pnorm) {
                 float ss = 0.f;
 #pragma unroll
-                for (int i = 0; i < 32; ++i) ss = fmaf(v[i], v[i], ss);
+                for (int i = 0; i < 32; ++i) {
+                    const float x = xt[i * 65 + lane];
+                    ss = fmaf(x, x, ss);
+                }
                 ss = wave_sum_canon(ss);
-                const float inv = 1.0f / sqrtf(ss / (float)QE_D + QE_RMS_EPS);
-#pragma unroll
-                for (int i = 0; i < 32; ++i) v[i] = (v[i] * inv) * s_pn[(lane >> 1) * 65 + (lane & 1) * 32 + i];
+                if (lane == 0) s_inv[t] = 1.0f / sqrtf(ss / (float)QE_D + QE_RMS_EPS);
             }
-#pragma unroll
-            for (int i = 0; i < 32; ++i) xt[i * 64 + lane] = v[i]; // all reads of the wave precede
-            lane_quant_store(v, s_xq + t * QE_D + lane * 32, s_xs + t * 64 + lane);
-            if (last && blockIdx.x == 0 && a.xn_out) {
-#pragma unroll
-                for (int i = 0; i < 32; ++i) a.xn_out[(size_t)t * QE_D + lane * 32 + i] = v[i];
+        }
+        __syncthreads();
+        for (int t = 0; t < T; ++t) {
+            float *xt = s_xn + t * DEC_XSTR;
+            const int e = 2 * tid;
+            float v0 = xt[xpos(e)], v1 = xt[xpos(e + 1)];
+            if (pnorm) {
+                const float inv = s_inv[t];
+                v0 = (v0 * inv) * s_pn[(e >> 6) * 65 + (e & 63)];
+                v1 = (v1 * inv) * s_pn[(e >> 6) * 65 + (e & 63) + 1];
             }
+            xt[xpos(e)] = v0;
+            xt[xpos(e + 1)] = v1;
+            float dq;
+            const float id = quant_scale_inv(max16(fmaxf(fabsf(v0), fabsf(v1))), dq);
+            *(uint16_t *)(s_xq + t * QE_D + e) =
+                (uint16_t)((unsigned)(uint8_t)quant_one(v0, id) | ((unsigned)(uint8_t)quant_one(v1, id) << 8));
+            if ((tid & 15) == 0) s_xs[t * 64 + (tid >> 4)] = dq;
+            if (last && blockIdx.x == 0 && a.xn_out) *(float2 *)(a.xn_out + (size_t)t * QE_D + e) = make_float2(v0, v1);
         }
         __syncthreads();
         for (int task = task0; task < N_RTASK; task += (int)gridDim.x * NWV) {
@@ -348,7 +361,7 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
                 for (int t = 0; t < T; ++t) {
                     float acc = 0.f;
 #pragma unroll
-                    for (int i = 0; i < 32; ++i) acc = fmaf(wr[i], s_xn[t * DEC_XSTR + i * 64 + lane], acc);
+                    for (int i = 0; i < 32; ++i) acc = fmaf(wr[i], s_xn[t * DEC_XSTR + i * 65 + lane], acc);
                     acc = wave_sum_canon(acc);
                     if (lane < REP) ST_A(EX + lane * EX_TOTAL + EX_L + t * QE_ROUTER_ROWS + task, pack_tv(add_bias ? acc + b : acc, tagR));
                 }
@@ -379,7 +392,7 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
                     float ag = 0.f, au = 0.f;
 #pragma unroll
                     for (int i = 0; i < 32; ++i) {
-                        const float xv = s_xn[t * DEC_XSTR + i * 64 + lane];
+                        const float xv = s_xn[t * DEC_XSTR + i * 65 + lane];
                         ag = fmaf(wg[i], xv, ag);
                         au = fmaf(wu[i], xv, au);
                     }
@@ -483,6 +496,7 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
         //   else:           JU = 32, 64 rows; wave w -> 4 rows, 16 lanes per row, a lane
         //                   holds blocks c + 16 i.  h quantised per 32 rows, published int8.
         const int JU = mode16 ? 16 : 32, upi = QE_FF_EXP / JU, nunits = nitems * upi;
+        auto no_prefetch = []() {};
         for (int unit = blockIdx.x; unit < nunits; unit += gridDim.x) {
             const int4 it = s_items[unit / upi];
             const int j0 = (unit % upi) * JU;
@@ -491,11 +505,11 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
             if (mode16) {
                 const int rw = (wv & 7) * 2 + (lane >> 5);
                 unit_rows<2>(base + (size_t)(j0 + rw) * QE_GU_ROW_BYTES, lane & 31, (up ? JU : 0) + rw, it, s_pairs,
-                             s_xq, s_xs, s_gu, d_prefetch);
+                             s_xq, s_xs, s_gu, no_prefetch);
             } else {
                 const int rw = (wv & 7) * 4 + (lane >> 4);
                 unit_rows<4>(base + (size_t)(j0 + rw) * QE_GU_ROW_BYTES, l16, (up ? JU : 0) + rw, it, s_pairs,
-                             s_xq, s_xs, s_gu, d_prefetch);
+                             s_xq, s_xs, s_gu, no_prefetch);
             }
             __syncthreads();
             if (mode16) {
@@ -542,21 +556,24 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
             s_hsh[i] = tv_val(w[0]);
         }
         if (mode16) { // fp32 h of the 8 pairs -> LDS, then int8 per 32 rows
+            // thread = 4 consecutive h of one pair, 8 lanes per 32-block (quant_x per block)
             static_assert(8 * QE_FF_EXP == 4 * NTH, "h of the 8 pairs: four words per thread");
             uint64_t w[4];
-            read_tv<4>(EXr + EX_HF + tid, NTH, tagG, w, true, a.err);
+            read_tv<4>(EXr + EX_HF + 4 * tid, 1, tagG, w, true, a.err);
+            float h[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) { // (pair, block) rows of 33 floats
-                const int e = tid + i * NTH;
-                s_hf[(e >> 5) * 33 + (e & 31)] = tv_val(w[i]);
-            }
-            __syncthreads();
-            if (tid < 8 * 16) { // thread (pair, block)
-                float v[32];
+            for (int i = 0; i < 4; ++i) h[i] = tv_val(w[i]);
+            float am = fmaxf(fmaxf(fabsf(h[0]), fabsf(h[1])), fmaxf(fabsf(h[2]), fabsf(h[3])));
+            am = fmaxf(am, dpp_f<QE_DPP_XOR1>(am));
+            am = fmaxf(am, dpp_f<QE_DPP_XOR2>(am));
+            am = fmaxf(am, dpp_f<QE_DPP_HMIRROR>(am));
+            float dq;
+            const float id = quant_scale_inv(am, dq);
+            unsigned q = 0;
 #pragma unroll
-                for (int i = 0; i < 32; ++i) v[i] = s_hf[tid * 33 + i];
-                lane_quant_store(v, s_hq + tid * 32, s_hs + tid);
-            }
+            for (int i = 0; i < 4; ++i) q |= (unsigned)(uint8_t)quant_one(h[i], id) << (8 * i);
+            *(unsigned *)(s_hq + 4 * tid) = q;
+            if ((tid & 7) == 0) s_hs[tid >> 3] = dq;
         } else {
             for (int task = tid; task < np * 16; task += NTH) { // (pair, 32-block): 8 code words + 1 scale
                 const int p = task >> 4, b = task & 15;

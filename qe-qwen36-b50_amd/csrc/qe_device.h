@@ -126,6 +126,23 @@ QE_DEV float wave_max(float v) {
     rows32(__float_as_uint(max32(v)), a, b);
     return fmaxf(__uint_as_float(a), __uint_as_float(b));
 }
+// u32 maximum over the wave; the DPP moves use bound_ctrl (every source lane
+// exists in these patterns) so they can fold into the v_max_u32 that uses them.
+template <int CTRL> QE_DEV unsigned dpp_ub(unsigned v) {
+    return (unsigned)__builtin_amdgcn_mov_dpp((int)v, CTRL, 0xf, 0xf, true);
+}
+QE_DEV unsigned umax32(unsigned a, unsigned b) { return a > b ? a : b; }
+QE_DEV unsigned wave_max_u32(unsigned v) {
+    v = umax32(v, dpp_ub<QE_DPP_XOR1>(v));
+    v = umax32(v, dpp_ub<QE_DPP_XOR2>(v));
+    v = umax32(v, dpp_ub<QE_DPP_HMIRROR>(v));
+    v = umax32(v, dpp_ub<QE_DPP_MIRROR>(v));
+    unsigned a, b;
+    rows16(v, a, b);
+    v = umax32(a, b);
+    rows32(v, a, b);
+    return umax32(a, b);
+}
 QE_DEV uint64_t umax64(uint64_t a, uint64_t b) { return a > b ? a : b; }
 template <int CTRL> QE_DEV uint64_t dpp64(uint64_t v) {
     return ((uint64_t)dpp_u<CTRL>((unsigned)(v >> 32)) << 32) | dpp_u<CTRL>((unsigned)v);
@@ -166,19 +183,28 @@ QE_DEV float silu_mul(float g, float u) { return g / (1.f + expf(-g)) * u; }
 // maximum logit first; ties go to the smaller (e % 16, e / 16), the order the
 // reference's 16-lane reduction produces.  Lane l holds e = l + 64 j.
 // ===========================================================================
+// Order-preserving u32 image of a float (-0 folded onto +0 by the caller).
+QE_DEV unsigned f2ord(float v) {
+    const unsigned u = __float_as_uint(v);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+QE_DEV float ord2f(unsigned o) { return __uint_as_float((o & 0x80000000u) ? (o & 0x7fffffffu) : ~o); }
+
 // v[j] = logit of expert lane + 64 j; lg_sh = logit 256 (shared-expert gate).
-// Each round: one wave max of the values, then ballots of the lanes holding
-// it; a single holder wins, several (a tie) go to the smallest key
-// (e % 16) * 16 + e / 16.  -0 and +0 compare equal, as in the reference.
-// The softmax weights run one per lane; their sum keeps the reference's
-// order k = 0..7.
+// Each round: one wave max of the values (as order-preserving u32, -0 folded
+// onto +0, so equal logits compare equal as in the reference), then ballots of
+// the lanes holding it; a single holder wins, several (a tie) go to the
+// smallest key (e % 16) * 16 + e / 16.  The softmax weights run one per lane;
+// their sum keeps the reference's order k = 0..7.
 QE_DEV void wave_topk_vals(const float v_in[4], float lg_sh, int lane, int32_t *ids, float *wts, float *shg) {
-    float v[4] = {v_in[0], v_in[1], v_in[2], v_in[3]};
+    unsigned v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = f2ord(v_in[j] + 0.0f);
     float sel[QE_K_USED];
     int id[QE_K_USED];
 #pragma unroll
     for (int k = 0; k < QE_K_USED; ++k) {
-        const float m = wave_max(fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])));
+        const unsigned m = wave_max_u32(umax32(umax32(v[0], v[1]), umax32(v[2], v[3])));
         uint64_t b[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) b[j] = __ballot(v[j] == m);
@@ -195,11 +221,11 @@ QE_DEV void wave_topk_vals(const float v_in[4], float lg_sh, int lane, int32_t *
                     if (key < bkey) { bkey = key; e = ee; }
                 }
         }
-        sel[k] = m;
+        sel[k] = ord2f(m);
         id[k] = e;
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-            if (64 * j + lane == e) v[j] = -INFINITY;
+            if (64 * j + lane == e) v[j] = 0u; // below every ordered float
     }
     float mine = sel[0];
     int myid = id[0];
