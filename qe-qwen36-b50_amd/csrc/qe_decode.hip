@@ -306,8 +306,8 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
         __syncthreads();
         // RMSNorm (wave_norm_chunk's arithmetic, spread over the workgroup): wave t
         // takes the residual rows of token t and its sum of squares in the
-        // canonical order (lane = 32-element chunk); then every thread scales,
-        // stores in place and quantises 2 elements per token (16 lanes per block).
+        // canonical order (lane = 32-element chunk); then threads scale, store in
+        // place and quantise 8 elements each (4 lanes per 32-block).
         if (wv < T) {
             const int t = wv;
             const float *xt = s_xn + t * DEC_XSTR;
@@ -327,23 +327,37 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
             }
         }
         __syncthreads();
-        for (int t = 0; t < T; ++t) {
+        for (int w = tid; w < T * 256; w += NTH) { // 8 elements of token t per thread, 4 lanes per block
+            const int t = w >> 8, e = 8 * (w & 255);
             float *xt = s_xn + t * DEC_XSTR;
-            const int e = 2 * tid;
-            float v0 = xt[xpos(e)], v1 = xt[xpos(e + 1)];
+            float v[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = xt[xpos(e + i)];
             if (pnorm) {
                 const float inv = s_inv[t];
-                v0 = (v0 * inv) * s_pn[(e >> 6) * 65 + (e & 63)];
-                v1 = (v1 * inv) * s_pn[(e >> 6) * 65 + (e & 63) + 1];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) v[i] = (v[i] * inv) * s_pn[(e >> 6) * 65 + (e & 63) + i];
             }
-            xt[xpos(e)] = v0;
-            xt[xpos(e + 1)] = v1;
+            float am = 0.f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                xt[xpos(e + i)] = v[i];
+                am = fmaxf(am, fabsf(v[i]));
+            }
+            am = fmaxf(am, dpp_f<QE_DPP_XOR1>(am));
+            am = fmaxf(am, dpp_f<QE_DPP_XOR2>(am));
             float dq;
-            const float id = quant_scale_inv(max16(fmaxf(fabsf(v0), fabsf(v1))), dq);
-            *(uint16_t *)(s_xq + t * QE_D + e) =
-                (uint16_t)((unsigned)(uint8_t)quant_one(v0, id) | ((unsigned)(uint8_t)quant_one(v1, id) << 8));
-            if ((tid & 15) == 0) s_xs[t * 64 + (tid >> 4)] = dq;
-            if (last && blockIdx.x == 0 && a.xn_out) *(float2 *)(a.xn_out + (size_t)t * QE_D + e) = make_float2(v0, v1);
+            const float id = quant_scale_inv(am, dq);
+            unsigned q[2] = {0u, 0u};
+#pragma unroll
+            for (int i = 0; i < 8; ++i) q[i >> 2] |= (unsigned)(uint8_t)quant_one(v[i], id) << (8 * (i & 3));
+            *(uint2 *)(s_xq + t * QE_D + e) = make_uint2(q[0], q[1]);
+            if ((w & 3) == 0) s_xs[t * 64 + (e >> 5)] = dq;
+            if (last && blockIdx.x == 0 && a.xn_out) {
+                float4 *o = (float4 *)(a.xn_out + (size_t)t * QE_D + e);
+                o[0] = make_float4(v[0], v[1], v[2], v[3]);
+                o[1] = make_float4(v[4], v[5], v[6], v[7]);
+            }
         }
         __syncthreads();
         for (int task = task0; task < N_RTASK; task += (int)gridDim.x * NWV) {
