@@ -6,7 +6,7 @@
 #include "qe_device.h"
 
 #define QE_SMALL_T 8   /* calls of up to this many tokens take the persistent decode kernel */
-#define QE_MFMA_MC 32 /* pairs per work item of the prefill MFMA grouped GEMMs (two 16-row tiles) */
+#define QE_MFMA_MC 32 /* pairs per work item of the prefill MFMA grouped GEMMs (up to two 16-row tiles) */
 
 
 // One layer's weights inside the context.

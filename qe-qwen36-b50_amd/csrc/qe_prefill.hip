@@ -91,9 +91,9 @@ QE_DEV void transpose_rows4(uint32_t d[4]) {
 
 template <bool GU> struct ExpertSmem {
     static constexpr int NB = (GU ? QE_D : QE_FF_EXP) / 32;
-    float xs[2][NB][16];       // activation scale per (tile, block, row)
-    uint16_t dw[4][NB][16][4]; // fp16 weight scale per (wave, block, n, group)
-    int pair[32];
+    float xs[QE_MFMA_MC / 16][NB][16]; // activation scale per (tile, block, row)
+    uint16_t dw[4][NB][16][4];         // fp16 weight scale per (wave, block, n, group)
+    int pair[QE_MFMA_MC];
 };
 
 template <bool GU, int NT>
@@ -125,17 +125,18 @@ __device__ __forceinline__ void expert_tile(const GemmTileArgs &a, const int4 it
             for (int j = 0; j < 8; ++j) s_dw[wv][8 * i + j][n][c] = (uint16_t)(w4[j >> 1] >> (16 * (j & 1)));
         }
     }
-    if (tid < 32) s_pair[tid] = tid < it.z ? a.pairs[it.y + tid] : -1;
+    if (tid < QE_MFMA_MC) s_pair[tid] = tid < it.z ? a.pairs[it.y + tid] : -1;
     __syncthreads();
     {
-        float v[32 * NB / 256];
+        constexpr int NV = 16 * NT * NB / 256; // scales of the item's NT tiles, per thread
+        float v[NV];
 #pragma unroll
-        for (int k = 0; k < 32 * NB / 256; ++k) {
+        for (int k = 0; k < NV; ++k) {
             const int i = tid + 256 * k, m = i / NB, b = i % NB, p = s_pair[m];
             v[k] = p < 0 ? 0.f : a.as[(size_t)(p / a.a_row_div) * NB + b];
         }
 #pragma unroll
-        for (int k = 0; k < 32 * NB / 256; ++k) {
+        for (int k = 0; k < NV; ++k) {
             const int i = tid + 256 * k, m = i / NB, b = i % NB;
             s_xs[m >> 4][b][m & 15] = v[k];
         }
@@ -154,25 +155,25 @@ __device__ __forceinline__ void expert_tile(const GemmTileArgs &a, const int4 it
         rowc[c] = row_of(wv, c, n);
         boff[c] = (uint32_t)rowc[c] * RB + 16 * g;
     }
-    uint32_t aoff[2];
+    uint32_t aoff[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
         const int p = s_pair[16 * t + n];
         aoff[t] = (uint32_t)((p < 0 ? s_pair[0] : p) / a.a_row_div) * KD + 16 * g; // padding rows: scale 0
     }
 
-    float acc[4][2][4];
+    float acc[4][NT][4];
 #pragma unroll
     for (int c = 0; c < 4; ++c)
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
+        for (int t = 0; t < NT; ++t)
 #pragma unroll
             for (int i = 0; i < 4; ++i) acc[c][t][i] = 0.f;
 
     // Ring: quad slot qs of turn ch holds blocks 8 ch + 4 qs .. +3; pair slot
     // ps holds blocks 8 ch + 2 ps, +1.  Refills wrap to turn (ch + 1) % NCH.
     uint4 rq[2][4];      // raw codes, per quad slot and column group
-    uint4 ra[4][2];      // activations, per pair slot and tile
+    uint4 ra[4][NT];     // activations, per pair slot and tile
     auto ld128 = [](__amdgpu_buffer_rsrc_t r, uint32_t vo, int so) {
         const qe_u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, vo, so, 0);
         return make_uint4(v.x, v.y, v.z, v.w);
@@ -223,12 +224,6 @@ __device__ __forceinline__ void expert_tile(const GemmTileArgs &a, const int4 it
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int s = 4 * qs + j, b = 8 * ch + s, ps = s >> 1;
-                long av[2];
-#pragma unroll
-                for (int t = 0; t < NT; ++t) {
-                    const uint4 v = ra[ps][t];
-                    av[t] = (s & 1) ? (long)(((uint64_t)v.w << 32) | v.z) : (long)(((uint64_t)v.y << 32) | v.x);
-                }
                 long bv[4];
 #pragma unroll
                 for (int c = 0; c < 4; ++c) {
@@ -236,44 +231,46 @@ __device__ __forceinline__ void expert_tile(const GemmTileArgs &a, const int4 it
                     const uint32_t lo = nl4_lookup4(q & 0x0f0f0f0fu), hi = nl4_lookup4((q >> 4) & 0x0f0f0f0fu);
                     bv[c] = (long)(((uint64_t)hi << 32) | lo);
                 }
-                typedef int i32x4 __attribute__((ext_vector_type(4)));
-                i32x4 P[2][4];
-#pragma unroll
-                for (int t = 0; t < NT; ++t)
-#pragma unroll
-                    for (int c = 0; c < 4; ++c) {
-                        const i32x4 zero = {0, 0, 0, 0};
-                        P[t][c] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[t], bv[c], zero, 0, 0, 0);
-                    }
-                if (s & 1) {
-                    // last read of the pair slot done: refill it (see above)
-                    uint32_t dep;
-                    if (NT == 2)
-                        asm volatile("v_mov_b32 %0, 0" : "=v"(dep)
-                                     : "v"(P[0][0][0]), "v"(P[0][1][0]), "v"(P[0][2][0]), "v"(P[0][3][0]),
-                                       "v"(P[1][0][0]), "v"(P[1][1][0]), "v"(P[1][2][0]), "v"(P[1][3][0]));
-                    else
-                        asm volatile("v_mov_b32 %0, 0" : "=v"(dep)
-                                     : "v"(P[0][0][0]), "v"(P[0][1][0]), "v"(P[0][2][0]), "v"(P[0][3][0]));
-                    load_a(nx, ps, dep);
-                    __builtin_amdgcn_sched_barrier(0);
-                }
                 const uint2 d2 = *(const uint2 *)&s_dw[wv][b][n][0];
                 float dw[4];
                 dw[0] = f16_bits_to_f32((uint16_t)(d2.x & 0xffffu));
                 dw[1] = f16_bits_to_f32((uint16_t)(d2.x >> 16));
                 dw[2] = f16_bits_to_f32((uint16_t)(d2.y & 0xffffu));
                 dw[3] = f16_bits_to_f32((uint16_t)(d2.y >> 16));
+                // per tile: four exact block dots on the matrix cores, then the fp32 scaling
 #pragma unroll
                 for (int t = 0; t < NT; ++t) {
+                    const uint4 v = ra[ps][t];
+                    const long av = (s & 1) ? (long)(((uint64_t)v.w << 32) | v.z) : (long)(((uint64_t)v.y << 32) | v.x);
+                    typedef int i32x4 __attribute__((ext_vector_type(4)));
+                    i32x4 P[4];
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) {
+                        const i32x4 zero = {0, 0, 0, 0};
+                        P[c] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bv[c], zero, 0, 0, 0);
+                    }
                     const float4 x4 = *(const float4 *)&s_xs[t][b][4 * g];
 #pragma unroll
                     for (int c = 0; c < 4; ++c) {
-                        acc[c][t][0] = fmaf((float)P[t][c][0], x4.x * dw[c], acc[c][t][0]);
-                        acc[c][t][1] = fmaf((float)P[t][c][1], x4.y * dw[c], acc[c][t][1]);
-                        acc[c][t][2] = fmaf((float)P[t][c][2], x4.z * dw[c], acc[c][t][2]);
-                        acc[c][t][3] = fmaf((float)P[t][c][3], x4.w * dw[c], acc[c][t][3]);
+                        acc[c][t][0] = fmaf((float)P[c][0], x4.x * dw[c], acc[c][t][0]);
+                        acc[c][t][1] = fmaf((float)P[c][1], x4.y * dw[c], acc[c][t][1]);
+                        acc[c][t][2] = fmaf((float)P[c][2], x4.z * dw[c], acc[c][t][2]);
+                        acc[c][t][3] = fmaf((float)P[c][3], x4.w * dw[c], acc[c][t][3]);
                     }
+                }
+                if (s & 1) {
+                    // last read of the pair slot done (every tile's accumulators
+                    // depend on it): refill the slot (see above)
+                    uint32_t dep;
+                    if (NT == 1)
+                        asm volatile("v_mov_b32 %0, 0" : "=v"(dep) : "v"(acc[0][0][0]));
+                    else if (NT == 2)
+                        asm volatile("v_mov_b32 %0, 0" : "=v"(dep) : "v"(acc[0][0][0]), "v"(acc[0][NT - 1][0]));
+                    else
+                        asm volatile("v_mov_b32 %0, 0" : "=v"(dep)
+                                     : "v"(acc[0][0][0]), "v"(acc[0][1][0]), "v"(acc[0][NT - 2][0]), "v"(acc[0][NT - 1][0]));
+                    load_a(nx, ps, dep);
+                    __builtin_amdgcn_sched_barrier(0);
                 }
             }
         }
@@ -283,8 +280,7 @@ __device__ __forceinline__ void expert_tile(const GemmTileArgs &a, const int4 it
     if (GU) {
         const int jb = blockIdx.y * 4 + wv; // 32-block of h
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            if (t >= NT) break;
+        for (int t = 0; t < NT; ++t) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const float h0 = silu_mul(acc[0][t][i], acc[2][t][i]);
@@ -304,8 +300,7 @@ __device__ __forceinline__ void expert_tile(const GemmTileArgs &a, const int4 it
         }
     } else {
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            if (t >= NT) break;
+        for (int t = 0; t < NT; ++t) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int p = s_pair[16 * t + 4 * g + i];
@@ -325,6 +320,7 @@ __global__ __launch_bounds__(256, 2) void k_expert_mfma(GemmTileArgs a) {
     __shared__ ExpertSmem<GU> sm;
     if ((int)blockIdx.x >= *a.n_items) return;
     const int4 it = a.items[blockIdx.x];
+    static_assert(QE_MFMA_MC == 32, "items of up to two 16-row tiles");
     if (it.z > 16)
         expert_tile<GU, 2>(a, it, sm);
     else
