@@ -297,9 +297,9 @@ int qe_moe_get_logits(qe_moe_ctx *c, int T, float *logits, void *stream) {
 }
 
 static const char *const k_prof_names[QP_N] = {
-    "k_decode", "k_normq", "k_router_split", "k_shared_gu", "k_topk",
-    "k_disp_hist+k_disp_scatter", "k_expert_mfma<gate_up>+k_expert_mfma<down>", "unused", "unused",
-    "k_shared_dn", "k_combine"};
+    "k_decode", "k_normq", "k_router_shgu", "unused", "k_topk",
+    "k_disp_scatter", "k_expert_gu+k_expert_dn(+shared down)", "unused", "unused",
+    "unused", "k_combine"};
 
 int qe_moe_profile(qe_moe_ctx *c, int enable) {
     if (!c) return fail(QE_ERR_ARG, "profile: bad argument");

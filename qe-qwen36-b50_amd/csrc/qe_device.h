@@ -196,7 +196,8 @@ QE_DEV float ord2f(unsigned o) { return __uint_as_float((o & 0x80000000u) ? (o &
 // the lanes holding it; a single holder wins, several (a tie) go to the
 // smallest key (e % 16) * 16 + e / 16.  The softmax weights run one per lane;
 // their sum keeps the reference's order k = 0..7.
-QE_DEV void wave_topk_vals(const float v_in[4], float lg_sh, int lane, int32_t *ids, float *wts, float *shg) {
+// Returns, in lane k < 8, the k-th selected expert.
+QE_DEV int wave_topk_vals(const float v_in[4], float lg_sh, int lane, int32_t *ids, float *wts, float *shg) {
     unsigned v[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) v[j] = f2ord(v_in[j] + 0.0f);
@@ -241,6 +242,7 @@ QE_DEV void wave_topk_vals(const float v_in[4], float lg_sh, int lane, int32_t *
         wts[lane] = ex / s;
     }
     if (lane == QE_K_USED) *shg = 1.f / (1.f + expf(-lg_sh));
+    return myid;
 }
 QE_DEV void wave_topk(const float *lg, int lane, int32_t *ids, float *wts, float *shg) {
     float v[4];

@@ -6,6 +6,7 @@
 #include "qe_device.h"
 
 #define QE_SMALL_T 8   /* calls of up to this many tokens take the persistent decode kernel */
+#define RT_SPLIT 8     /* router K split: subtrees of 64 / RT_SPLIT chunks, merged by k_topk */
 #define QE_MFMA_MC 32 /* pairs per work item of the prefill MFMA grouped GEMMs (up to two 16-row tiles) */
 
 
@@ -99,7 +100,8 @@ hipError_t qe_launch_layer(const QeLayerPtrs &L, const QeScratch &S, const float
                            float *out, int T, hipStream_t st);
 hipError_t qe_launch_dispatch(const QeScratch &S, int T, hipStream_t st);
 hipError_t qe_launch_expert_mfma(const QeLayerPtrs &L, const QeScratch &S, int T, hipStream_t st);
-hipError_t qe_launch_shared_mfma(const QeLayerPtrs &L, const QeScratch &S, int T, bool gate_up, hipStream_t st);
+hipError_t qe_launch_router_shgu(const QeLayerPtrs &L, const QeScratch &S, int T, hipStream_t st);
+
 hipError_t qe_launch_synth_layer(uint8_t *arena_l, float *router_l, uint8_t *sh_gu_l, uint8_t *sh_dn_l,
                                  float *post_norm_l, uint64_t seed, int layer, hipStream_t st);
 hipError_t qe_launch_synth_x(float *out, uint64_t seed, int inst, int64_t n, hipStream_t st);

@@ -3,9 +3,9 @@
 // Launch plans (host side in qe_api.hip):
 //  * small T (<= QE_SMALL_T tokens): the persistent kernel in qe_decode.hip;
 //  * large T (prefill, Engine::moe_batched, engine/qe.cpp:1957-2047):
-//      k_normq, k_router_split, the shared-expert MFMA GEMMs and the
-//      routed-expert MFMA grouped GEMMs of qe_prefill.hip, k_topk,
-//      k_disp_hist, k_disp_scatter, k_combine.
+//      k_normq; k_router_shgu (router tiles + shared gate/up tiles), k_topk
+//      (+ dispatch histogram), k_disp_scatter, the routed-expert MFMA grouped
+//      GEMMs of qe_prefill.hip (shared down rides with routed down), k_combine.
 // Routing (RMSNorm, router dot products, top-8) follows the checker's
 // canonical fp32 order exactly; expert products use exact int8 block dots
 // with fp32 block scaling, so they agree with the CPU path to fp32 rounding.
@@ -16,8 +16,9 @@
 // ===========================================================================
 // wave per token: xn, xq, xs
 __global__ __launch_bounds__(256) void k_normq(const float *x, int T, const float *post_norm, float *xn, int8_t *xqp,
-                                               float *xs, _Float16 *xhl) {
+                                               float *xs, _Float16 *xhl, int32_t *chunk_hist, int nch) {
     const int lane = threadIdx.x & 63, t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if ((int)blockIdx.x < nch) chunk_hist[blockIdx.x * QE_N_EXPERT + threadIdx.x] = 0; // dispatch histogram
     if (t >= T) return;
     float v[32];
     load32(x + (size_t)t * QE_D + lane * 32, v);
@@ -29,105 +30,21 @@ __global__ __launch_bounds__(256) void k_normq(const float *x, int T, const floa
     lane_quant_store_opnd(v, xqp + (size_t)t * QE_D, lane, xs + (size_t)t * (QE_D / 32) + lane);
 }
 
-// Router logits 0..255 in the canonical fp32 order, tiled:
-// C[m][n] = sum_k xn[m][k] W[n][k].  Canonical order: per 32-wide k chunk an fma
-// chain from 0, chunk sums merged by the pairwise tree (chunks (c, c+1), then
-// pairs of pairs, ...).  The K range is split eight ways along that tree: split
-// z computes the 8-chunk subtree [8z, 8z+8) exactly, and k_topk forms the top
-// three levels ((s0 + s1) + (s2 + s3)) + ((s4 + s5) + (s6 + s7)) -- bit-identical
-// to the unsplit order.  Row 256 (the shared-expert gate) is one canonical wave
-// dot per token in k_topk.  Tile 64 tokens x 64 rows, 256 threads, 4 x 4 outputs
-// per thread; chunks are double-buffered in LDS, the next one loaded into
-// registers while the current one is multiplied.
-#define RT_SPLIT 8
-__global__ __launch_bounds__(256) void k_router_split(const float *xn, int T, const float *W, float *part) {
-    constexpr int NCH = 64 / RT_SPLIT; // chunks per split
-    __shared__ float As[2][32][68];
-    __shared__ float Bs[2][32][68];
-    const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
-    const int m0 = blockIdx.y * 64, n0 = blockIdx.x * 64, z = blockIdx.z;
-    const int lr = tid >> 2, lk = (tid & 3) * 8; // loader: row lr of the tile, 8 k values
-    const bool a_ok = m0 + lr < T;
-    const float *ap = xn + (size_t)(a_ok ? m0 + lr : 0) * QE_D + z * NCH * 32 + lk;
-    const float *bp = W + (size_t)(n0 + lr) * QE_D + z * NCH * 32 + lk;
-    float4 pa[2], pb[2];
-    auto fetch = [&](int cl) {
-        const float4 *a4 = (const float4 *)(ap + cl * 32), *b4 = (const float4 *)(bp + cl * 32);
-        pa[0] = a_ok ? a4[0] : make_float4(0.f, 0.f, 0.f, 0.f);
-        pa[1] = a_ok ? a4[1] : make_float4(0.f, 0.f, 0.f, 0.f);
-        pb[0] = b4[0];
-        pb[1] = b4[1];
-    };
-    auto stage = [&](int buf) {
-        const float va[8] = {pa[0].x, pa[0].y, pa[0].z, pa[0].w, pa[1].x, pa[1].y, pa[1].z, pa[1].w};
-        const float vb[8] = {pb[0].x, pb[0].y, pb[0].z, pb[0].w, pb[1].x, pb[1].y, pb[1].z, pb[1].w};
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            As[buf][lk + i][lr] = va[i];
-            Bs[buf][lk + i][lr] = vb[i];
-        }
-    };
-    fetch(0);
-    stage(0);
-    __syncthreads();
-    float st[4][4][4];
-#pragma unroll 1
-    for (int cl = 0; cl < NCH; ++cl) {
-        const int buf = cl & 1;
-        if (cl + 1 < NCH) fetch(cl + 1);
-        float acc[4][4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) acc[i][j] = 0.f;
-#pragma unroll
-        for (int kk = 0; kk < 32; ++kk) {
-            const float4 av = *(const float4 *)&As[buf][kk][ty * 4];
-            const float4 bv = *(const float4 *)&Bs[buf][kk][tx * 4];
-            const float ar[4] = {av.x, av.y, av.z, av.w}, br[4] = {bv.x, bv.y, bv.z, bv.w};
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(ar[i], br[j], acc[i][j]);
-        }
-        bool carry = true; // pairwise-tree merge of chunk cl
-#pragma unroll
-        for (int l = 0; l < 4; ++l) {
-            if (carry) {
-                if (cl & (1 << l)) {
-#pragma unroll
-                    for (int i = 0; i < 4; ++i)
-#pragma unroll
-                        for (int j = 0; j < 4; ++j) acc[i][j] = st[l][i][j] + acc[i][j];
-                } else {
-#pragma unroll
-                    for (int i = 0; i < 4; ++i)
-#pragma unroll
-                        for (int j = 0; j < 4; ++j) st[l][i][j] = acc[i][j];
-                    carry = false;
-                }
-            }
-        }
-        if (cl + 1 < NCH) stage(buf ^ 1);
-        __syncthreads();
-    }
-    constexpr int TOP = NCH == 8 ? 3 : NCH == 16 ? 4 : 2;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int m = m0 + ty * 4 + i;
-        if (m >= T) continue;
-        *(float4 *)&part[((size_t)z * T + m) * QE_N_EXPERT + n0 + tx * 4] =
-            make_float4(st[TOP][i][0], st[TOP][i][1], st[TOP][i][2], st[TOP][i][3]);
-    }
-}
 static_assert(RT_SPLIT == 8, "k_topk merges eight router partials");
 
-// Wave per token: logits (router partials merged + bias; row 256 as a canonical
-// wave dot), then top-8, weights and the shared gate (engine/qe.cpp:1454-1483).
+// Wave per token, 4 tokens per workgroup: logits (router partials merged +
+// bias; row 256 as a canonical wave dot), then top-8, weights and the shared
+// gate (engine/qe.cpp:1454-1483).  The workgroup then adds its 32 expert ids
+// to the dispatch histogram of its 1024-pair chunk (zeroed by k_normq), one
+// global add per distinct expert.
 __global__ __launch_bounds__(256) void k_topk(const float *part, const float *xn, const float *W, const float *bias,
-                                              int T, float *logits, int32_t *ids, float *wts, float *shg) {
+                                              int T, float *logits, int32_t *ids, float *wts, float *shg,
+                                              int32_t *chunk_hist) {
+    __shared__ int s_h[QE_N_EXPERT];
     const int lane = threadIdx.x & 63, t = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (t >= T) return;
+    if (threadIdx.x < QE_N_EXPERT) s_h[threadIdx.x] = 0;
+    __syncthreads();
+    if (t < T) {
     const size_t n = (size_t)T * QE_N_EXPERT;
     float v[4];
 #pragma unroll
@@ -156,7 +73,13 @@ __global__ __launch_bounds__(256) void k_topk(const float *part, const float *xn
     }
     const float lg = wave_sum_canon(acc);
     if (lane == 0) logits[(size_t)t * QE_ROUTER_ROWS + QE_N_EXPERT] = lg;
-    wave_topk_vals(v, lg, lane, ids + t * QE_K_USED, wts + t * QE_K_USED, shg + t);
+    const int e = wave_topk_vals(v, lg, lane, ids + t * QE_K_USED, wts + t * QE_K_USED, shg + t);
+    if (lane < QE_K_USED) atomicAdd(&s_h[e], 1);
+    }
+    __syncthreads();
+    static_assert(1024 % (4 * QE_K_USED) == 0, "a workgroup's pairs lie in one dispatch chunk");
+    if (s_h[threadIdx.x])
+        atomicAdd(&chunk_hist[(blockIdx.x * 4 * QE_K_USED / 1024) * QE_N_EXPERT + threadIdx.x], s_h[threadIdx.x]);
 }
 
 // Dispatch pass 1: per-chunk (1024 pairs) expert histogram.
@@ -247,6 +170,7 @@ __global__ __launch_bounds__(1024) void k_disp_scatter(const int32_t *ids, int n
     }
 }
 
+
 // out[t][r] = x2 + shg*sd + sum_k yp[t*8+k][r]  (engine/qe.cpp:2036-2044)
 __global__ __launch_bounds__(256) void k_combine(QeCombineArgs a) {
     const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
@@ -294,34 +218,29 @@ hipError_t qe_launch_layer(const QeLayerPtrs &L, const QeScratch &S, const float
                            float *out, int T, hipStream_t st) {
     const float *pn = norm ? L.post_norm : nullptr;
     QeCombineArgs da{T, S.yp, S.sd, S.shg, x2, out};
-    const int mt = (T + 63) / 64;
     {
         QE_PROF(QP_NORMQ);
-        k_normq<<<(T + 3) / 4, 256, 0, st>>>(xin, T, pn, S.xn, S.xqp, S.xs, S.xhl);
+        k_normq<<<(T + 3) / 4, 256, 0, st>>>(xin, T, pn, S.xn, S.xqp, S.xs, S.xhl, S.chunk_hist,
+                                              (T * QE_K_USED + 1023) / 1024);
     }
     {
         QE_PROF(QP_ROUTER);
-        k_router_split<<<dim3(QE_N_EXPERT / 64, mt, RT_SPLIT), 256, 0, st>>>(S.xn, T, L.router, S.rpart);
-    }
-    {
-        QE_PROF(QP_SHGU);
-        (void)qe_launch_shared_mfma(L, S, T, true, st);
+        (void)qe_launch_router_shgu(L, S, T, st);
     }
     {
         QE_PROF(QP_TOPK);
-        k_topk<<<(T + 3) / 4, 256, 0, st>>>(S.rpart, S.xn, L.router, L.bias, T, S.logits, S.ids, S.wts, S.shg);
+        k_topk<<<(T + 3) / 4, 256, 0, st>>>(S.rpart, S.xn, L.router, L.bias, T, S.logits, S.ids, S.wts, S.shg,
+                                             S.chunk_hist);
     }
     {
-        QE_PROF(QP_DISPATCH);
-        (void)qe_launch_dispatch(S, T, st);
+        QE_PROF(QP_DISPATCH); // the histogram came with k_topk
+        const int np = T * QE_K_USED, nch = (np + 1023) / 1024;
+        k_disp_scatter<<<nch, 1024, 0, st>>>(S.ids, np, S.chunk_hist, nch, QE_MFMA_MC, S.off, S.pairs, S.items,
+                                              S.n_items);
     }
     {
-        QE_PROF(QP_GU);
+        QE_PROF(QP_GU); // routed gate/up, then routed down + shared down
         (void)qe_launch_expert_mfma(L, S, T, st);
-    }
-    {
-        QE_PROF(QP_SHDN);
-        (void)qe_launch_shared_mfma(L, S, T, false, st);
     }
     {
         QE_PROF(QP_COMBINE);

@@ -97,7 +97,7 @@ template <bool GU> struct ExpertSmem {
 };
 
 template <bool GU, int NT>
-__device__ __forceinline__ void expert_tile(const GemmTileArgs &a, const int4 it, ExpertSmem<GU> &sm) {
+__device__ __forceinline__ void expert_tile(const GemmTileArgs &a, const int4 it, const int yb, ExpertSmem<GU> &sm) {
     constexpr int KD = GU ? QE_D : QE_FF_EXP;  // reduction length
     constexpr int NB = KD / 32;                // K blocks
     constexpr int NCH = NB / 8;                // ring turns (two quads each)
@@ -107,8 +107,7 @@ __device__ __forceinline__ void expert_tile(const GemmTileArgs &a, const int4 it
     auto &s_pair = sm.pair;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, n = lane & 15, g = lane >> 4;
     auto row_of = [&](int w, int c, int nn) {
-        return GU ? (c < 2 ? 0 : QE_FF_EXP) + (blockIdx.y * 4 + w) * 32 + 16 * (c & 1) + nn
-                  : blockIdx.y * 256 + w * 64 + 16 * c + nn;
+        return GU ? (c < 2 ? 0 : QE_FF_EXP) + (yb * 4 + w) * 32 + 16 * (c & 1) + nn : yb * 256 + w * 64 + 16 * c + nn;
     };
     const uint8_t *ebase = a.arena + (size_t)it.x * QE_EXPERT_BYTES + (GU ? 0 : QE_EXPERT_DOWN_OFF);
     {
@@ -278,7 +277,7 @@ __device__ __forceinline__ void expert_tile(const GemmTileArgs &a, const int4 it
 
     // lane holds rows 16 t + 4 g + i, column n of each group
     if (GU) {
-        const int jb = blockIdx.y * 4 + wv; // 32-block of h
+        const int jb = yb * 4 + wv; // 32-block of h
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
 #pragma unroll
@@ -315,29 +314,20 @@ __device__ __forceinline__ void expert_tile(const GemmTileArgs &a, const int4 it
 }
 
 // One launch per GEMM; an item of <= 16 pairs runs the one-tile body.
-template <bool GU>
-__global__ __launch_bounds__(256, 2) void k_expert_mfma(GemmTileArgs a) {
-    __shared__ ExpertSmem<GU> sm;
-    if ((int)blockIdx.x >= *a.n_items) return;
-    const int4 it = a.items[blockIdx.x];
+template <bool GU> QE_DEV void expert_item(const GemmTileArgs &a, int item, int yb, ExpertSmem<GU> &sm) {
+    if (item >= *a.n_items) return;
+    const int4 it = a.items[item];
     static_assert(QE_MFMA_MC == 32, "items of up to two 16-row tiles");
     if (it.z > 16)
-        expert_tile<GU, 2>(a, it, sm);
+        expert_tile<GU, 2>(a, it, yb, sm);
     else
-        expert_tile<GU, 1>(a, it, sm);
+        expert_tile<GU, 1>(a, it, yb, sm);
+}
+__global__ __launch_bounds__(256, 2) void k_expert_gu(GemmTileArgs a) {
+    __shared__ ExpertSmem<true> sm;
+    expert_item<true>(a, blockIdx.x, blockIdx.y, sm);
 }
 
-hipError_t qe_launch_expert_mfma(const QeLayerPtrs &L, const QeScratch &S, int T, hipStream_t st) {
-    const int np = T * QE_K_USED;
-    const int max_items = np / QE_MFMA_MC + QE_N_EXPERT;
-    GemmTileArgs g{};
-    g.arena = L.arena; g.pairs = S.pairs; g.items = S.items; g.n_items = S.n_items; g.wts = S.wts;
-    g.aq = S.xqp; g.a_bytes = T * QE_D; g.as = S.xs; g.a_row_div = QE_K_USED; g.hq = S.hqp; g.hs = S.hs;
-    k_expert_mfma<true><<<dim3(max_items, QE_FF_EXP / 128), 256, 0, st>>>(g);
-    g.aq = S.hqp; g.a_bytes = np * QE_FF_EXP; g.as = S.hs; g.a_row_div = 1; g.yp = S.yp;
-    k_expert_mfma<false><<<dim3(max_items, QE_D / 256), 256, 0, st>>>(g);
-    return hipGetLastError();
-}
 
 // ===========================================================================
 // Shared expert (Q8 weights, fp32 activations; engine/qe.cpp:2469, :1656,
@@ -376,21 +366,123 @@ QE_DEV void sh_block(const qe_u32x4 a[4], qe_u32x4 w, float dw, qe_float16v &acc
     p = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(qe_half8, a[3]), b1, p, 0, 0, 0);
 #pragma unroll
     for (int i = 0; i < 16; ++i) acc[i] = fmaf(dw, p[i], acc[i]);
+    // scale now: left alone the compiler defers every block's scaling to the end,
+    // keeping all the block products live
+    asm volatile("" : "+v"(acc));
 }
 QE_DEV float half_of(const qe_u32x4 s[2], int b) { // fp16 scale b of 16 packed in two dwordx4
     const uint32_t w = s[b >> 3][(b >> 1) & 3];
     return f16_bits_to_f32((uint16_t)((b & 1) ? w >> 16 : w & 0xffffu));
 }
 
-__global__ __launch_bounds__(256) void k_shared_gu(const _Float16 *xhl, int T, const uint8_t *W, _Float16 *hhl) {
+// Router logits 0..255 in the canonical fp32 order, tiled:
+// C[m][n] = sum_k xn[m][k] W[n][k].  Canonical order: per 32-wide k chunk an fma
+// chain from 0, chunk sums merged by the pairwise tree (chunks (c, c+1), then
+// pairs of pairs, ...).  The K range is split eight ways along that tree: split
+// z computes the 8-chunk subtree [8z, 8z+8) exactly, and k_topk forms the top
+// three levels ((s0 + s1) + (s2 + s3)) + ((s4 + s5) + (s6 + s7)) -- bit-identical
+// to the unsplit order.  Row 256 (the shared-expert gate) is one canonical wave
+// dot per token in k_topk.  Tile 64 tokens x 64 rows, 256 threads, 4 x 4 outputs
+// per thread; chunks are double-buffered in LDS, the next one loaded into
+// registers while the current one is multiplied.
+struct RouterSmem {
+    float As[2][32][68];
+    float Bs[2][32][68];
+};
+QE_DEV void router_tile(const float *xn, int T, const float *W, float *part, int n_tile, int m_tile, int z,
+                        RouterSmem &sm) {
+    constexpr int NCH = 64 / RT_SPLIT; // chunks per split
+    auto &As = sm.As;
+    auto &Bs = sm.Bs;
+    const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+    const int m0 = m_tile * 64, n0 = n_tile * 64;
+    const int lr = tid >> 2, lk = (tid & 3) * 8; // loader: row lr of the tile, 8 k values
+    const bool a_ok = m0 + lr < T;
+    const float *ap = xn + (size_t)(a_ok ? m0 + lr : 0) * QE_D + z * NCH * 32 + lk;
+    const float *bp = W + (size_t)(n0 + lr) * QE_D + z * NCH * 32 + lk;
+    float4 pa[2], pb[2];
+    auto fetch = [&](int cl) {
+        const float4 *a4 = (const float4 *)(ap + cl * 32), *b4 = (const float4 *)(bp + cl * 32);
+        pa[0] = a_ok ? a4[0] : make_float4(0.f, 0.f, 0.f, 0.f);
+        pa[1] = a_ok ? a4[1] : make_float4(0.f, 0.f, 0.f, 0.f);
+        pb[0] = b4[0];
+        pb[1] = b4[1];
+    };
+    auto stage = [&](int buf) {
+        const float va[8] = {pa[0].x, pa[0].y, pa[0].z, pa[0].w, pa[1].x, pa[1].y, pa[1].z, pa[1].w};
+        const float vb[8] = {pb[0].x, pb[0].y, pb[0].z, pb[0].w, pb[1].x, pb[1].y, pb[1].z, pb[1].w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            As[buf][lk + i][lr] = va[i];
+            Bs[buf][lk + i][lr] = vb[i];
+        }
+    };
+    fetch(0);
+    stage(0);
+    __syncthreads();
+    float st[4][4][4];
+#pragma unroll 1
+    for (int cl = 0; cl < NCH; ++cl) {
+        const int buf = cl & 1;
+        if (cl + 1 < NCH) fetch(cl + 1);
+        float acc[4][4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[i][j] = 0.f;
+#pragma unroll
+        for (int kk = 0; kk < 32; ++kk) {
+            const float4 av = *(const float4 *)&As[buf][kk][ty * 4];
+            const float4 bv = *(const float4 *)&Bs[buf][kk][tx * 4];
+            const float ar[4] = {av.x, av.y, av.z, av.w}, br[4] = {bv.x, bv.y, bv.z, bv.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(ar[i], br[j], acc[i][j]);
+        }
+        bool carry = true; // pairwise-tree merge of chunk cl
+#pragma unroll
+        for (int l = 0; l < 4; ++l) {
+            if (carry) {
+                if (cl & (1 << l)) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) acc[i][j] = st[l][i][j] + acc[i][j];
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) st[l][i][j] = acc[i][j];
+                    carry = false;
+                }
+            }
+        }
+        if (cl + 1 < NCH) stage(buf ^ 1);
+        __syncthreads();
+    }
+    constexpr int TOP = NCH == 8 ? 3 : NCH == 16 ? 4 : 2;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int m = m0 + ty * 4 + i;
+        if (m >= T) continue;
+        *(float4 *)&part[((size_t)z * T + m) * QE_N_EXPERT + n0 + tx * 4] =
+            make_float4(st[TOP][i][0], st[TOP][i][1], st[TOP][i][2], st[TOP][i][3]);
+    }
+}
+
+struct ShguSmem {
+    float red[4][2][16][64];
+};
+QE_DEV void shgu_tile(const _Float16 *xhl, int T, const uint8_t *W, _Float16 *hhl, int m_tile, int j_tile, ShguSmem &sm) {
     constexpr uint32_t RB = QE_SH_GU_ROW_BYTES;
-    __shared__ float red[4][2][16][64];
+    auto &red = sm.red;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, c = lane & 31, kh = lane >> 5;
-    const int m0 = blockIdx.x * 32, j0 = blockIdx.y * 32, kb0 = wv * SH_GU_KB;
+    const int m0 = m_tile * 32, j0 = j_tile * 32, kb0 = wv * SH_GU_KB;
     const __amdgpu_buffer_rsrc_t ra =
         __builtin_amdgcn_make_buffer_rsrc((void *)xhl, (short)0, ((T + 31) & ~31) * QE_D * 4, 0x00020000);
     const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void *)W, (short)0, (int)QE_SH_GU_BYTES, 0x00020000);
-    const uint32_t a_off = (uint32_t)(blockIdx.x * (QE_D / 32) + kb0) * 4096 + lane * 16;
+    const uint32_t a_off = (uint32_t)(m_tile * (QE_D / 32) + kb0) * 4096 + lane * 16;
     const uint32_t g_off = (uint32_t)(j0 + c) * RB, u_off = g_off + QE_FF_SH * RB;
     qe_u32x4 sg[2], su[2];
 #pragma unroll
@@ -399,7 +491,7 @@ __global__ __launch_bounds__(256) void k_shared_gu(const _Float16 *xhl, int T, c
         su[i] = sh_ld(rw, u_off + QE_D + 2 * kb0 + 16 * i);
     }
     qe_float16v ag = {}, au = {};
-    constexpr int DEPTH = 4;
+    constexpr int DEPTH = 3;
     qe_u32x4 ra_[DEPTH][4], rg[DEPTH], ru[DEPTH];
     auto load = [&](int b) {
         const int s = b % DEPTH;
@@ -442,15 +534,46 @@ __global__ __launch_bounds__(256) void k_shared_gu(const _Float16 *xhl, int T, c
     }
 }
 
-__global__ __launch_bounds__(256) void k_shared_dn(const _Float16 *hhl, int T, const uint8_t *W, float *out) {
+
+// Router split tiles and shared gate/up tiles in one launch, interleaved
+// (even workgroups route, odd ones run the shared expert while both kinds
+// remain), so the fp32 VALU router and the matrix-core shared GEMM share the
+// CUs instead of running back to back.
+__global__ __launch_bounds__(256) void k_router_shgu(const float *xn, const _Float16 *xhl, int T, const float *Wr,
+                                                     const uint8_t *Wg, float *part, _Float16 *hhl) {
+    __shared__ union {
+        RouterSmem r;
+        ShguSmem s;
+    } sm;
+    const int mt64 = (T + 63) / 64, mt32 = (T + 31) / 32;
+    const int nr = (QE_N_EXPERT / 64) * mt64 * RT_SPLIT, ns = mt32 * (QE_FF_SH / 32);
+    const int b = blockIdx.x, both = 2 * (nr < ns ? nr : ns);
+    bool router;
+    int idx;
+    if (b < both) {
+        router = (b & 1) == 0;
+        idx = b >> 1;
+    } else {
+        router = nr > ns;
+        idx = b - both + (both >> 1);
+    }
+    if (router) {
+        const int n_tile = idx % (QE_N_EXPERT / 64), rest = idx / (QE_N_EXPERT / 64);
+        router_tile(xn, T, Wr, part, n_tile, rest % mt64, rest / mt64, sm.r);
+    } else {
+        shgu_tile(xhl, T, Wg, hhl, idx % mt32, idx / mt32, sm.s);
+    }
+}
+
+QE_DEV void shdn_tile(const _Float16 *hhl, int T, const uint8_t *W, float *out, int m_tile, int n_tile) {
     constexpr uint32_t RB = QE_SH_DN_ROW_BYTES;
     constexpr int NB = QE_FF_SH / 32;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, c = lane & 31, kh = lane >> 5;
-    const int m0 = blockIdx.x * 32, n = blockIdx.y * 128 + wv * 32 + c;
+    const int m0 = m_tile * 32, n = n_tile * 128 + wv * 32 + c;
     const __amdgpu_buffer_rsrc_t ra =
         __builtin_amdgcn_make_buffer_rsrc((void *)hhl, (short)0, ((T + 31) & ~31) * QE_FF_SH * 4, 0x00020000);
     const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void *)W, (short)0, (int)QE_SH_DN_BYTES, 0x00020000);
-    const uint32_t a_off = (uint32_t)blockIdx.x * NB * 4096 + lane * 16;
+    const uint32_t a_off = (uint32_t)m_tile * NB * 4096 + lane * 16;
     const uint32_t w_off = (uint32_t)n * RB;
     qe_u32x4 sw[2];
 #pragma unroll
@@ -481,10 +604,36 @@ __global__ __launch_bounds__(256) void k_shared_dn(const _Float16 *hhl, int T, c
     }
 }
 
-hipError_t qe_launch_shared_mfma(const QeLayerPtrs &L, const QeScratch &S, int T, bool gate_up, hipStream_t st) {
-    const unsigned mt = (unsigned)((T + 31) / 32);
-    _Float16 *hhl = (_Float16 *)S.shgu;
-    if (gate_up) k_shared_gu<<<dim3(mt, QE_FF_SH / 32), 256, 0, st>>>(S.xhl, T, L.sh_gu, hhl);
-    else k_shared_dn<<<dim3(mt, QE_D / 128), 256, 0, st>>>(hhl, T, L.sh_dn, S.sd);
+// Routed down items and shared down tiles in one launch: the routed items
+// (ordered by row group, then item) come first, the shared tiles fill the CUs
+// as the routed work drains.
+__global__ __launch_bounds__(256, 2) void k_expert_dn(GemmTileArgs a, int max_items, const _Float16 *hhl, int T,
+                                                      const uint8_t *Wsd, float *sd) {
+    __shared__ ExpertSmem<false> sm;
+    const int nr = max_items * (QE_D / 256), b = blockIdx.x;
+    if (b < nr) {
+        expert_item<false>(a, b % max_items, b / max_items, sm);
+    } else {
+        const int s = b - nr, mt = (T + 31) / 32;
+        shdn_tile(hhl, T, Wsd, sd, s % mt, s / mt);
+    }
+}
+
+hipError_t qe_launch_router_shgu(const QeLayerPtrs &L, const QeScratch &S, int T, hipStream_t st) {
+    const int nr = (QE_N_EXPERT / 64) * ((T + 63) / 64) * RT_SPLIT, ns = ((T + 31) / 32) * (QE_FF_SH / 32);
+    k_router_shgu<<<nr + ns, 256, 0, st>>>(S.xn, S.xhl, T, L.router, L.sh_gu, S.rpart, (_Float16 *)S.shgu);
+    return hipGetLastError();
+}
+
+hipError_t qe_launch_expert_mfma(const QeLayerPtrs &L, const QeScratch &S, int T, hipStream_t st) {
+    const int np = T * QE_K_USED;
+    const int max_items = np / QE_MFMA_MC + QE_N_EXPERT;
+    GemmTileArgs g{};
+    g.arena = L.arena; g.pairs = S.pairs; g.items = S.items; g.n_items = S.n_items; g.wts = S.wts;
+    g.aq = S.xqp; g.a_bytes = T * QE_D; g.as = S.xs; g.a_row_div = QE_K_USED; g.hq = S.hqp; g.hs = S.hs;
+    k_expert_gu<<<dim3(max_items, QE_FF_EXP / 128), 256, 0, st>>>(g);
+    g.aq = S.hqp; g.a_bytes = np * QE_FF_EXP; g.as = S.hs; g.a_row_div = 1; g.yp = S.yp;
+    const int nsh = ((T + 31) / 32) * (QE_D / 128);
+    k_expert_dn<<<max_items * (QE_D / 256) + nsh, 256, 0, st>>>(g, max_items, (const _Float16 *)S.shgu, T, L.sh_dn, S.sd);
     return hipGetLastError();
 }
