@@ -132,22 +132,36 @@ __global__ __launch_bounds__(1024) void k_disp_scatter(const int32_t *ids, int n
     if (blockIdx.x == 0) {
         if (tid < 256) off_out[tid] = s_off[tid];
         if (tid == 0) off_out[QE_N_EXPERT] = s_scan[255];
-        // work items: ceil(cnt/tc) per expert
-        __shared__ int s_ni[QE_N_EXPERT];
-        if (tid < 256) s_ni[tid] = (s_cnt[tid] + tc - 1) / tc;
+        // work items of <= tc pairs per expert: first every item of more than
+        // tc / 2 pairs (whole items and large remainders), then the small
+        // remainders, each class in expert order -- the longer items start first
+        __shared__ int s_nb[QE_N_EXPERT], s_ns[QE_N_EXPERT];
+        const int cnt = tid < 256 ? s_cnt[tid] : 0, full = cnt / tc, rem = cnt % tc;
+        const int nb = full + (rem > tc / 2), ns = rem > 0 && rem <= tc / 2;
+        if (tid < 256) {
+            s_nb[tid] = nb;
+            s_ns[tid] = ns;
+        }
         __syncthreads();
         for (int o = 1; o < 256; o <<= 1) {
-            int v = 0;
-            if (tid < 256 && tid >= o) v = s_ni[tid - o];
+            int vb = 0, vs = 0;
+            if (tid < 256 && tid >= o) {
+                vb = s_nb[tid - o];
+                vs = s_ns[tid - o];
+            }
             __syncthreads();
-            if (tid < 256) s_ni[tid] += v;
+            if (tid < 256) {
+                s_nb[tid] += vb;
+                s_ns[tid] += vs;
+            }
             __syncthreads();
         }
         if (tid < 256) {
-            const int nie = (s_cnt[tid] + tc - 1) / tc, base = s_ni[tid] - nie;
-            for (int c = 0; c < nie; ++c)
-                items[base + c] = make_int4(tid, s_off[tid] + c * tc, min(tc, s_cnt[tid] - c * tc), 0);
-            if (tid == 255) *n_items = s_ni[255];
+            const int bb = s_nb[tid] - nb, total_b = s_nb[255];
+            for (int c = 0; c < full; ++c) items[bb + c] = make_int4(tid, s_off[tid] + c * tc, tc, 0);
+            if (rem > tc / 2) items[bb + full] = make_int4(tid, s_off[tid] + full * tc, rem, 0);
+            if (ns) items[total_b + s_ns[tid] - 1] = make_int4(tid, s_off[tid] + full * tc, rem, 0);
+            if (tid == 255) *n_items = total_b + s_ns[255];
         }
     }
     const int p = blockIdx.x * 1024 + tid;

@@ -323,9 +323,10 @@ template <bool GU> QE_DEV void expert_item(const GemmTileArgs &a, int item, int 
     else
         expert_tile<GU, 1>(a, it, yb, sm);
 }
+// Workgroup (row group y, item) with y fastest: an item's row groups run together.
 __global__ __launch_bounds__(256, 2) void k_expert_gu(GemmTileArgs a) {
     __shared__ ExpertSmem<true> sm;
-    expert_item<true>(a, blockIdx.x, blockIdx.y, sm);
+    expert_item<true>(a, blockIdx.y, blockIdx.x, sm);
 }
 
 
@@ -605,14 +606,14 @@ QE_DEV void shdn_tile(const _Float16 *hhl, int T, const uint8_t *W, float *out, 
 }
 
 // Routed down items and shared down tiles in one launch: the routed items
-// (ordered by row group, then item) come first, the shared tiles fill the CUs
-// as the routed work drains.
+// (item, then row group) come first, the shared tiles fill the CUs as the
+// routed work drains.
 __global__ __launch_bounds__(256, 2) void k_expert_dn(GemmTileArgs a, int max_items, const _Float16 *hhl, int T,
                                                       const uint8_t *Wsd, float *sd) {
     __shared__ ExpertSmem<false> sm;
     const int nr = max_items * (QE_D / 256), b = blockIdx.x;
     if (b < nr) {
-        expert_item<false>(a, b % max_items, b / max_items, sm);
+        expert_item<false>(a, b / (QE_D / 256), b % (QE_D / 256), sm);
     } else {
         const int s = b - nr, mt = (T + 31) / 32;
         shdn_tile(hhl, T, Wsd, sd, s % mt, s / mt);
@@ -631,7 +632,7 @@ hipError_t qe_launch_expert_mfma(const QeLayerPtrs &L, const QeScratch &S, int T
     GemmTileArgs g{};
     g.arena = L.arena; g.pairs = S.pairs; g.items = S.items; g.n_items = S.n_items; g.wts = S.wts;
     g.aq = S.xqp; g.a_bytes = T * QE_D; g.as = S.xs; g.a_row_div = QE_K_USED; g.hq = S.hqp; g.hs = S.hs;
-    k_expert_gu<<<dim3(max_items, QE_FF_EXP / 128), 256, 0, st>>>(g);
+    k_expert_gu<<<dim3(QE_FF_EXP / 128, max_items), 256, 0, st>>>(g);
     g.aq = S.hqp; g.a_bytes = np * QE_FF_EXP; g.as = S.hs; g.a_row_div = 1; g.yp = S.yp;
     const int nsh = ((T + 31) / 32) * (QE_D / 128);
     k_expert_dn<<<max_items * (QE_D / 256) + nsh, 256, 0, st>>>(g, max_items, (const _Float16 *)S.shgu, T, L.sh_dn, S.sd);
