@@ -59,7 +59,7 @@ QE_DEV int xpos(int e) { return (e & 31) * 65 + (e >> 5); } // raw x element e o
 #define L_GU L_U                                    //   G: f32 [64 rows][8 pairs] gate/up dots of a unit
 #define L_HQ (L_U + 64 * 8 * 4)                     //   D: int8 [T*8][512] quantised h
 #define L_HS (L_HQ + DEC_T * 8 * QE_FF_EXP)         //   D: f32 [T*8][16] its block scales
-#define L_Y (L_HS + DEC_T * 8 * 16 * 4)             //   D: f32 [8 rows][2 halves][T] partials, [8][T] sd
+#define L_Y (L_HS + DEC_T * 8 * 16 * 4)             //   D: f32 [8 rows][2 halves][T] routed partials
 #define L_U_END (L_U + DEC_T * DEC_XSTR * 4)
 #define L_XQ L_U_END                                // int8 [T][2048]   quantised xn
 #define L_XS (L_XQ + DEC_T * QE_D)                  // f32 [T][64]      its block scales
@@ -74,8 +74,9 @@ QE_DEV int xpos(int e) { return (e & 31) * 65 + (e >> 5); } // raw x element e o
 #define L_SHG (L_WTS + 64 * 4)                      // f32 [8]
 #define L_MISC (L_SHG + 8 * 4)                      // int [16]
 #define L_INV (L_MISC + 16 * 4)                     // f32 [8]          1 / rms of each token
-#define L_TOTAL (L_INV + 8 * 4)
-static_assert(L_Y + (8 * 2 * DEC_T + 8 * DEC_T) * 4 <= L_U_END, "D-stage LDS must fit in the union");
+#define L_SD (L_INV + 8 * 4)                        // f32 [4][8][T]    shared-expert output of the D rows
+#define L_TOTAL (L_SD + 4 * 8 * DEC_T * 4)
+static_assert(L_Y + 8 * 2 * DEC_T * 4 <= L_U_END, "D-stage LDS must fit in the union");
 static_assert(64 * 8 * 4 <= L_HQ - L_U, "G-stage LDS must fit in front of the D buffers");
 static_assert(L_TOTAL <= 160 * 1024, "LDS budget of one workgroup per CU");
 
@@ -199,6 +200,7 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
     float *s_xn = (float *)(lds + L_XN);
     float *s_pn = (float *)(lds + L_PN);
     float *s_inv = (float *)(lds + L_INV);
+    float *s_sd = (float *)(lds + L_SD);
     float *s_gu = (float *)(lds + L_GU);
     int8_t *s_hq = (int8_t *)(lds + L_HQ);
     float *s_hs = (float *)(lds + L_HS);
@@ -559,15 +561,44 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
         // No counter: h is polled through its tags.  For T = 1 one word per unit
         // (its last row) is polled first, then everything is read with the tags
         // verified (a late word is re-read).
-        if (mode16 && tid < 256) {
-            uint64_t w[1];
-            poll_tv2<1>(EXr + EX_HF + (tid >> 5) * QE_FF_EXP + (tid & 31) * 16 + 15, 0, tagG, w, true, a.err);
-        }
         // shared-expert activations of every token: written in R, long landed by now
         for (int i = tid; i < T * QE_FF_SH; i += NTH) {
             uint64_t w[1];
             read_tv<1>(EXr + EX_HSH + i, 0, tagR, w, true, a.err);
             s_hsh[i] = tv_val(w[0]);
+        }
+        __syncthreads();
+        // The shared down rows of every D row group run first, while the routed
+        // h is still on its way: wave (rr, half 0), 16-lane group g takes tokens
+        // g, g + 4 of row rr.
+        if (half == 0) {
+            for (int m = 0; m < d_iters; ++m) {
+                const int rb = (blockIdx.x + m * gridDim.x) * 8;
+                if (rb >= QE_D) break;
+                if (m > 0) {
+                    const uint8_t *srow = sh_dn + (size_t)(rb + rr) * QE_SH_DN_ROW_BYTES;
+                    dq0 = ((const uint4 *)(srow + l16 * 32))[0];
+                    dq1 = ((const uint4 *)(srow + l16 * 32))[1];
+                    dsc = ((const uint16_t *)(srow + QE_FF_SH))[l16];
+                }
+                float w8[32];
+                unpack_i8x32(dq0, dq1, w8);
+                const float ssd = f16_bits_to_f32(dsc);
+                for (int t0 = 0; t0 < T; t0 += 4) {
+                    const int t = t0 + isub;
+                    float acc = 0.f;
+                    if (t < T) {
+#pragma unroll
+                        for (int i = 0; i < 32; ++i) acc = fmaf(w8[i], s_hsh[t * QE_FF_SH + l16 * 32 + i], acc);
+                    }
+                    const float sd = sum16(acc * ssd);
+                    if (l16 == 0 && t < T) s_sd[(m * 8 + rr) * DEC_T + t] = sd;
+                }
+            }
+        }
+        if (mode16 && tid < 256) {
+            uint64_t w[1];
+            poll_tv2<1>(EXr + EX_HF + (tid >> 5) * QE_FF_EXP + (tid & 31) * 16 + 15, 0, tagG, w, true, a.err);
         }
         if (mode16) { // fp32 h of the 8 pairs -> LDS, then int8 per 32 rows
             // thread = 4 consecutive h of one pair, 8 lanes per 32-block (quant_x per block)
@@ -644,31 +675,10 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
                 for (int t = 0; t < TM; ++t)
                     if (t < T) s_y[(rr * 2 + half) * DEC_T + t] = y[t];
             }
-            if (half == 0) { // shared down row r: 16-lane group g takes tokens g, g + 4
-                if (m > 0) {
-                    const uint8_t *srow = sh_dn + (size_t)r * QE_SH_DN_ROW_BYTES;
-                    dq0 = ((const uint4 *)(srow + l16 * 32))[0];
-                    dq1 = ((const uint4 *)(srow + l16 * 32))[1];
-                    dsc = ((const uint16_t *)(srow + QE_FF_SH))[l16];
-                }
-                float w8[32];
-                unpack_i8x32(dq0, dq1, w8);
-                const float ssd = f16_bits_to_f32(dsc);
-                for (int t0 = 0; t0 < T; t0 += 4) {
-                    const int t = t0 + isub;
-                    float acc = 0.f;
-                    if (t < T) {
-#pragma unroll
-                        for (int i = 0; i < 32; ++i) acc = fmaf(w8[i], s_hsh[t * QE_FF_SH + l16 * 32 + i], acc);
-                    }
-                    const float sd = sum16(acc * ssd);
-                    if (l16 == 0 && t < T) s_y[16 * DEC_T + rr * DEC_T + t] = sd;
-                }
-            }
             __syncthreads();
             if (tid < 8 * T) { // thread (row, token): combine
                 const int k = tid / T, t = tid % T, ro = rb + k;
-                const float sd = s_y[16 * DEC_T + k * DEC_T + t];
+                const float sd = s_sd[(m * 8 + k) * DEC_T + t];
                 const float yt = s_y[(k * 2) * DEC_T + t] + s_y[(k * 2 + 1) * DEC_T + t];
                 const float res = a.residual ? s_res[t * 32 + m * 8 + k] : 0.f;
                 const float out = (res + s_shg[t] * sd) + yt;

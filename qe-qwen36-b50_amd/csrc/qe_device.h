@@ -21,9 +21,13 @@ QE_DEV uint32_t nl4_lookup4(uint32_t idx /* 4 indices, one per byte, 0..15 */) {
     const uint32_t sel = ((idx >> 1) & 0x04040404u) | 0x03020100u;     // bit 3 -> take b
     return __builtin_amdgcn_perm(b, a, sel);
 }
+// Both nibbles of 4 code bytes; the bit-3 selector comes straight from the
+// code bytes (bits 3 and 7), without extracting the nibbles first.
 QE_DEV void nl4_decode_dword(uint32_t q, uint32_t &lo, uint32_t &hi) {
-    lo = nl4_lookup4(q & 0x0f0f0f0fu);
-    hi = nl4_lookup4((q >> 4) & 0x0f0f0f0fu);
+    const uint32_t il = q & 0x07070707u, ih = (q >> 4) & 0x07070707u;
+    const uint32_t sl = ((q >> 1) & 0x04040404u) | 0x03020100u, sh = ((q >> 5) & 0x04040404u) | 0x03020100u;
+    lo = __builtin_amdgcn_perm(__builtin_amdgcn_perm(QE_NL4_W3, QE_NL4_W2, il), __builtin_amdgcn_perm(QE_NL4_W1, QE_NL4_W0, il), sl);
+    hi = __builtin_amdgcn_perm(__builtin_amdgcn_perm(QE_NL4_W3, QE_NL4_W2, ih), __builtin_amdgcn_perm(QE_NL4_W1, QE_NL4_W0, ih), sh);
 }
 // Decoded 32-weight block: w[0..3] = elements 0..15, w[4..7] = elements 16..31,
 // each dword holding 4 consecutive elements.

@@ -226,8 +226,8 @@ __device__ __forceinline__ void expert_tile(const GemmTileArgs &a, const int4 it
                 long bv[4];
 #pragma unroll
                 for (int c = 0; c < 4; ++c) {
-                    const uint32_t q = cw[c][j];
-                    const uint32_t lo = nl4_lookup4(q & 0x0f0f0f0fu), hi = nl4_lookup4((q >> 4) & 0x0f0f0f0fu);
+                    uint32_t lo, hi;
+                    nl4_decode_dword(cw[c][j], lo, hi);
                     bv[c] = (long)(((uint64_t)hi << 32) | lo);
                 }
                 const uint2 d2 = *(const uint2 *)&s_dw[wv][b][n][0];
