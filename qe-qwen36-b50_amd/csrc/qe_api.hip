@@ -47,7 +47,7 @@ struct qe_moe_ctx {
     std::vector<void *> allocs;
 };
 
-static int dalloc(qe_moe_ctx *c, void **p, size_t bytes) {
+static int dalloc(qe_moe_ctx *c, void **p, size_t bytes, bool zero = true) {
     if (hipMalloc(p, bytes) != hipSuccess) {
         *p = nullptr;
         return fail(QE_ERR_OOM, "hipMalloc(%zu) failed", bytes);
@@ -55,7 +55,7 @@ static int dalloc(qe_moe_ctx *c, void **p, size_t bytes) {
     c->allocs.push_back(*p);
     // scratch starts as zeros: the padding rows of the prefill tiles are read
     // (never stored), and must hold finite values
-    if (hipMemset(*p, 0, bytes) != hipSuccess) return fail(QE_ERR_HIP, "hipMemset(%zu) failed", bytes);
+    if (zero && hipMemset(*p, 0, bytes) != hipSuccess) return fail(QE_ERR_HIP, "hipMemset(%zu) failed", bytes);
     return QE_OK;
 }
 
@@ -99,7 +99,7 @@ int qe_moe_create(int device, int n_layers, int t_max, qe_moe_ctx **out) {
     QeScratch &S = c->S;
 #define A(ptr, bytes) \
     if (rc == QE_OK) rc = dalloc(c, (void **)&(ptr), (bytes))
-    A(c->arena, L * QE_LAYER_EXPERT_BYTES);
+    if (rc == QE_OK) rc = dalloc(c, (void **)&c->arena, L * QE_LAYER_EXPERT_BYTES, false); // written by upload/synth
     A(c->router, L * QE_ROUTER_BYTES);
     A(c->bias, L * QE_N_EXPERT * 4);
     A(c->sh_gu, L * QE_SH_GU_BYTES);

@@ -147,6 +147,18 @@ QE_DEV unsigned wave_max_u32(unsigned v) {
     rows32(v, a, b);
     return umax32(a, b);
 }
+QE_DEV unsigned umin32(unsigned a, unsigned b) { return a < b ? a : b; }
+QE_DEV unsigned wave_min_u32(unsigned v) {
+    v = umin32(v, dpp_ub<QE_DPP_XOR1>(v));
+    v = umin32(v, dpp_ub<QE_DPP_XOR2>(v));
+    v = umin32(v, dpp_ub<QE_DPP_HMIRROR>(v));
+    v = umin32(v, dpp_ub<QE_DPP_MIRROR>(v));
+    unsigned a, b;
+    rows16(v, a, b);
+    v = umin32(a, b);
+    rows32(v, a, b);
+    return umin32(a, b);
+}
 QE_DEV uint64_t umax64(uint64_t a, uint64_t b) { return a > b ? a : b; }
 template <int CTRL> QE_DEV uint64_t dpp64(uint64_t v) {
     return ((uint64_t)dpp_u<CTRL>((unsigned)(v >> 32)) << 32) | dpp_u<CTRL>((unsigned)v);
@@ -196,9 +208,8 @@ QE_DEV float ord2f(unsigned o) { return __uint_as_float((o & 0x80000000u) ? (o &
 
 // v[j] = logit of expert lane + 64 j; lg_sh = logit 256 (shared-expert gate).
 // Each round: one wave max of the values (as order-preserving u32, -0 folded
-// onto +0, so equal logits compare equal as in the reference), then ballots of
-// the lanes holding it; a single holder wins, several (a tie) go to the
-// smallest key (e % 16) * 16 + e / 16.  The softmax weights run one per lane;
+// onto +0, so equal logits compare equal as in the reference), then one wave
+// min of the tie-break keys (e % 16) * 16 + e / 16 over the slots holding it.  The softmax weights run one per lane;
 // their sum keeps the reference's order k = 0..7.
 // Returns, in lane k < 8, the k-th selected expert.
 QE_DEV int wave_topk_vals(const float v_in[4], float lg_sh, int lane, int32_t *ids, float *wts, float *shg) {
@@ -207,30 +218,21 @@ QE_DEV int wave_topk_vals(const float v_in[4], float lg_sh, int lane, int32_t *i
     for (int j = 0; j < 4; ++j) v[j] = f2ord(v_in[j] + 0.0f);
     float sel[QE_K_USED];
     int id[QE_K_USED];
+    // tie-break key of slot j: (e % 16) * 16 + e / 16 with e = lane + 64 j
+    const unsigned key0 = (unsigned)((lane & 15) * 16 + (lane >> 4));
 #pragma unroll
     for (int k = 0; k < QE_K_USED; ++k) {
         const unsigned m = wave_max_u32(umax32(umax32(v[0], v[1]), umax32(v[2], v[3])));
-        uint64_t b[4];
+        // smallest key among the holders of m, by a second wave reduction
+        unsigned ck = 0xffffu;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) b[j] = __ballot(v[j] == m);
-        int e;
-        if (__popcll(b[0]) + __popcll(b[1]) + __popcll(b[2]) + __popcll(b[3]) == 1) {
-            const int j = b[0] ? 0 : b[1] ? 1 : b[2] ? 2 : 3;
-            e = 64 * j + __ffsll((long long)b[j]) - 1;
-        } else {
-            int bkey = 1 << 20;
-            e = 0;
-            for (int j = 0; j < 4; ++j)
-                for (uint64_t mk = b[j]; mk; mk &= mk - 1) {
-                    const int l = __ffsll((long long)mk) - 1, ee = 64 * j + l, key = (ee & 15) * 16 + (ee >> 4);
-                    if (key < bkey) { bkey = key; e = ee; }
-                }
-        }
+        for (int j = 3; j >= 0; --j) ck = v[j] == m ? key0 + 4 * j : ck;
+        const unsigned kmin = wave_min_u32(ck);
         sel[k] = ord2f(m);
-        id[k] = e;
+        id[k] = (int)((kmin & 15) * 16 + (kmin >> 4));
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-            if (64 * j + lane == e) v[j] = 0u; // below every ordered float
+            if (key0 + 4 * j == kmin) v[j] = 0u; // below every ordered float
     }
     float mine = sel[0];
     int myid = id[0];
