@@ -258,21 +258,23 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
         uint8_t *rw_lds = lds + L_RW + (wv & 3) * 8192;
         const bool rw_pref = wv < 4 && task0 < N_RTASK;
         if (rw_pref) {
-            auto dma16 = [&](const uint8_t *src, uint8_t *dst) { // 64 lanes x 16 B, lane i -> dst + 16 i
-                __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)(src + lane * 16),
+            // Lane i's 16 bytes land at dst + 16 i; the source is the i-th lane chunk's
+            // k-th 16 bytes, so the dot (lane = chunk) reads dst + 16 lane: no bank conflicts.
+            auto dma16 = [&](const uint8_t *src, uint8_t *dst) {
+                __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)src,
                                                  (__attribute__((address_space(3))) void *)dst, 16, 0, 0);
             };
-            if (task0 < QE_ROUTER_ROWS) {
+            if (task0 < QE_ROUTER_ROWS) { // chunk = 128 B of fp32
                 const uint8_t *row = (const uint8_t *)(router + (size_t)task0 * QE_D);
 #pragma unroll
-                for (int k = 0; k < 8; ++k) dma16(row + k * 1024, rw_lds + k * 1024);
-            } else {
+                for (int k = 0; k < 8; ++k) dma16(row + lane * 128 + k * 16, rw_lds + k * 1024);
+            } else { // chunk = 32 B of int8 per matrix
                 const int j = task0 - QE_ROUTER_ROWS;
                 const uint8_t *rg = sh_gu + (size_t)j * QE_SH_GU_ROW_BYTES, *ru = sh_gu + (size_t)(QE_FF_SH + j) * QE_SH_GU_ROW_BYTES;
 #pragma unroll
                 for (int k = 0; k < 2; ++k) {
-                    dma16(rg + k * 1024, rw_lds + k * 1024);
-                    dma16(ru + k * 1024, rw_lds + 2048 + k * 1024);
+                    dma16(rg + lane * 32 + k * 16, rw_lds + k * 1024);
+                    dma16(ru + lane * 32 + k * 16, rw_lds + 2048 + k * 1024);
                 }
                 __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)(rg + QE_D + lane * 2),
                                                  (__attribute__((address_space(3))) void *)(rw_lds + 4096), 2, 0, 0);
@@ -370,7 +372,7 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
                 float wr[32];
                 if (in_lds) {
 #pragma unroll
-                    for (int i = 0; i < 8; ++i) *(float4 *)(wr + 4 * i) = *(const float4 *)(rw_lds + lane * 128 + 16 * i);
+                    for (int i = 0; i < 8; ++i) *(float4 *)(wr + 4 * i) = *(const float4 *)(rw_lds + i * 1024 + lane * 16);
                 } else {
                     load32(router + (size_t)task * QE_D + lane * 32, wr);
                 }
@@ -386,10 +388,10 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
                 uint4 g0, g1, u0, u1;
                 float gsc, usc;
                 if (in_lds) {
-                    g0 = *(const uint4 *)(rw_lds + lane * 32);
-                    g1 = *(const uint4 *)(rw_lds + lane * 32 + 16);
-                    u0 = *(const uint4 *)(rw_lds + 2048 + lane * 32);
-                    u1 = *(const uint4 *)(rw_lds + 2048 + lane * 32 + 16);
+                    g0 = *(const uint4 *)(rw_lds + lane * 16);
+                    g1 = *(const uint4 *)(rw_lds + 1024 + lane * 16);
+                    u0 = *(const uint4 *)(rw_lds + 2048 + lane * 16);
+                    u1 = *(const uint4 *)(rw_lds + 3072 + lane * 16);
                     gsc = f16_bits_to_f32((uint16_t)*(const unsigned *)(rw_lds + 4096 + lane * 4));
                     usc = f16_bits_to_f32((uint16_t)*(const unsigned *)(rw_lds + 4096 + 256 + lane * 4));
                 } else {

@@ -162,6 +162,45 @@ def test_prefill_ragged_T(ctx, torch_cuda, T, norm):
     check_layer(L, g, x, norm=norm)
 
 
+def tied_layer(kind):
+    """Layer 1's synthetic weights with a router that forces equal logits."""
+    L = O.SynthLayer(SEED, 1)
+    R = L.router.copy()
+    if kind == "zero":  # every logit 0: top-8 is the tie order itself
+        R[:] = 0.0
+    else:  # experts 0, 1, 16, 32 share one (scaled-up) row: ties between large logits
+        R[0] *= 8.0
+        R[1] = R[16] = R[32] = R[0]
+    L.router = np.ascontiguousarray(R, np.float32)
+    return L
+
+
+@pytest.mark.parametrize("kind", ["zero", "dup"])
+@pytest.mark.parametrize("T", [1, 5, 64])
+def test_topk_ties_on_gpu(ctx, torch_cuda, kind, T):
+    # ties go to the smaller (e % 16, e / 16): all-equal logits select 0, 16, ..., 112
+    say(f"top-8 ties ({kind} router), T={T}")
+    L = tied_layer(kind)
+    ctx.synth_layer(1, SEED, None)
+    ctx.set_dense(1, router=L.router)
+    x = O.gen_x(SEED, 400 + T, T)
+    xd = torch_cuda.from_numpy(x).cuda()
+    y = torch_cuda.empty_like(xd)
+    ctx.forward_normed(1, xd, y, T)
+    torch_cuda.cuda.synchronize()
+    g = ctx.routing(T)
+    g["logits"] = ctx.logits(T)
+    g["out"] = y.cpu().numpy()
+    o = check_layer(L, g, x)
+    if kind == "zero":
+        assert (o["ids"] == np.arange(0, 128, 16)).all()
+    else:
+        tied = np.isin(o["ids"], [0, 1, 16, 32]).sum(axis=1)
+        say(f"  tokens with the tied group in their top-8: {(tied == 4).sum()} of {T}")
+    _layers.pop((1, None), None)
+    ctx.synth_layer(1, SEED, None)  # restore the synthetic router for later tests
+
+
 def test_dispatch_on_reference_routing_records(ctx, torch_cuda):
     import os
     torch = torch_cuda
