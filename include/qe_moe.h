@@ -120,6 +120,16 @@ int qe_moe_profile(qe_moe_ctx *ctx, int enable);
 int qe_moe_profile_read(qe_moe_ctx *ctx, double *ms, int *launches, int n);
 const char *qe_moe_profile_name(int id);
 
+/* Load the MoE tensors of pack layers pack_first .. pack_first + n_layers - 1
+ * from a weight pack (layout engine/pack.h:45-54) into context layers
+ * first_layer .. first_layer + n_layers - 1: blk.N.experts (256 NL4 blobs),
+ * post_norm, router + sh_gate (F32), sh_gate_proj + sh_up and sh_down (Q8).
+ * Replaces Pack (engine/qe.cpp:50-71) and the MoE part of Engine::Engine's
+ * uploads (engine/qe.cpp:1051-1057, :1172-1194).  A missing tensor, another
+ * format or a size mismatch returns QE_ERR_ARG (the reference exits).
+ * Synchronous: returns once the copies are done. */
+int qe_moe_load_pack(qe_moe_ctx *ctx, const char *path, int pack_first, int first_layer, int n_layers, void *stream);
+
 /* Device pointer of a layer's expert arena (256 blobs), for callers that fill
  * it in place. */
 int qe_moe_arena_ptr(qe_moe_ctx *ctx, int layer, void **dev);

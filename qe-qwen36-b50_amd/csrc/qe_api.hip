@@ -1,9 +1,14 @@
 // C ABI of the MoE block (include/qe_moe.h): context, flat expert arena,
 // per-layer dense weights, scratch, and the forward entry points.
+#include <fcntl.h>
 #include <stdarg.h>
 #include <stdio.h>
 #include <string.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
 
+#include <map>
 #include <string>
 #include <vector>
 
@@ -192,6 +197,113 @@ int qe_moe_set_dense(qe_moe_ctx *c, int layer, const float *post_norm, const flo
     if (sh_down) HIP_TRY(hipMemcpyAsync((void *)L.sh_dn, sh_down, QE_SH_DN_BYTES, k, s));
     if (!on_dev) HIP_TRY(hipStreamSynchronize(s)); /* host sources need not outlive the call */
     c->ready[layer] = 1;
+    return QE_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Pack-file loader.  File layout as engine/pack.h:45-54 (header "QE36PK01",
+// entry table of {name[96], fmt, rows, cols, n, off, bytes}); the MoE tensors
+// of layer N under the names Engine::Engine uploads (engine/qe.cpp:1051-1057):
+// blk.N.post_norm (F32), blk.N.router + blk.N.sh_gate (F32, appended as router
+// row 256), blk.N.sh_gate_proj + blk.N.sh_up (Q8, gate rows then up rows),
+// blk.N.sh_down (Q8), and blk.N.experts (256 NL4 blobs, engine/qe.cpp:1177).
+// Where the reference exits (engine/qe.cpp:57-67), this returns QE_ERR_ARG.
+// ---------------------------------------------------------------------------
+namespace {
+struct PackHeaderRaw {
+    char magic[8];
+    uint32_t n_entries, pad;
+    uint64_t table_off;
+};
+struct PackEntryRaw {
+    char name[96];
+    uint32_t fmt, rows, cols, n;
+    uint64_t off, bytes;
+};
+static_assert(sizeof(PackHeaderRaw) == 24 && sizeof(PackEntryRaw) == 128, "pack layout of engine/pack.h");
+enum { PK_F32 = 0, PK_Q8 = 1, PK_Q6 = 2, PK_NL4 = 3 };
+struct MappedFile {
+    uint8_t *base = nullptr;
+    size_t size = 0;
+    ~MappedFile() {
+        if (base) munmap(base, size);
+    }
+};
+}  // namespace
+
+int qe_moe_load_pack(qe_moe_ctx *c, const char *path, int pack_first, int first_layer, int n_layers, void *stream) {
+    if (!c || !path || pack_first < 0 || first_layer < 0 || n_layers <= 0 || first_layer + n_layers > c->n_layers)
+        return fail(QE_ERR_ARG, "qe_moe_load_pack: bad argument");
+    MappedFile f;
+    {
+        const int fd = open(path, O_RDONLY);
+        if (fd < 0) return fail(QE_ERR_ARG, "qe_moe_load_pack: cannot open %s", path);
+        struct stat st;
+        if (fstat(fd, &st) != 0 || st.st_size < (off_t)sizeof(PackHeaderRaw)) {
+            close(fd);
+            return fail(QE_ERR_ARG, "qe_moe_load_pack: %s is not a pack", path);
+        }
+        f.size = (size_t)st.st_size;
+        void *m = mmap(nullptr, f.size, PROT_READ, MAP_PRIVATE, fd, 0);
+        close(fd);
+        if (m == MAP_FAILED) return fail(QE_ERR_ARG, "qe_moe_load_pack: cannot map %s", path);
+        f.base = (uint8_t *)m;
+    }
+    PackHeaderRaw h;
+    memcpy(&h, f.base, sizeof h);
+    if (memcmp(h.magic, "QE36PK01", 8) != 0) return fail(QE_ERR_ARG, "qe_moe_load_pack: bad magic in %s", path);
+    if (h.table_off > f.size || (f.size - h.table_off) / sizeof(PackEntryRaw) < h.n_entries)
+        return fail(QE_ERR_ARG, "qe_moe_load_pack: entry table past the end of %s", path);
+    std::map<std::string, PackEntryRaw> ents;
+    for (uint32_t i = 0; i < h.n_entries; ++i) {
+        PackEntryRaw e;
+        memcpy(&e, f.base + h.table_off + (size_t)i * sizeof e, sizeof e);
+        e.name[sizeof e.name - 1] = 0;
+        if (e.off > f.size || e.bytes > f.size - e.off)
+            return fail(QE_ERR_ARG, "qe_moe_load_pack: entry %s past the end of the file", e.name);
+        ents[e.name] = e;
+    }
+    // one tensor by name, checked for format, size and (for experts) count
+    auto get = [&](const std::string &name, uint32_t fmt, size_t bytes, uint32_t n, const uint8_t **out) -> int {
+        auto it = ents.find(name);
+        if (it == ents.end()) return fail(QE_ERR_ARG, "qe_moe_load_pack: missing %s", name.c_str());
+        const PackEntryRaw &e = it->second;
+        if (e.fmt != fmt)
+            return fail(QE_ERR_ARG, "qe_moe_load_pack: %s has format %u, this build takes %u", name.c_str(), e.fmt, fmt);
+        if (e.bytes != bytes || e.n != n)
+            return fail(QE_ERR_ARG, "qe_moe_load_pack: %s holds %llu bytes (n = %u), expected %zu (n = %u)", name.c_str(),
+                        (unsigned long long)e.bytes, e.n, bytes, n);
+        *out = f.base + e.off;
+        return QE_OK;
+    };
+    HIP_TRY(hipSetDevice(c->device));
+    hipStream_t s = (hipStream_t)stream;
+    const hipMemcpyKind k = hipMemcpyHostToDevice;
+    for (int i = 0; i < n_layers; ++i) {
+        const int l = first_layer + i;
+        const std::string pre = "blk." + std::to_string(pack_first + i) + ".";
+        const uint8_t *pn, *rt, *sg, *gp, *up, *dn, *ex;
+        int rc;
+        if ((rc = get(pre + "post_norm", PK_F32, QE_D * 4, 1, &pn)) != QE_OK) return rc;
+        if ((rc = get(pre + "router", PK_F32, (size_t)QE_N_EXPERT * QE_D * 4, 1, &rt)) != QE_OK) return rc;
+        if ((rc = get(pre + "sh_gate", PK_F32, QE_D * 4, 1, &sg)) != QE_OK) return rc;
+        if ((rc = get(pre + "sh_gate_proj", PK_Q8, QE_SH_GU_BYTES / 2, 1, &gp)) != QE_OK) return rc;
+        if ((rc = get(pre + "sh_up", PK_Q8, QE_SH_GU_BYTES / 2, 1, &up)) != QE_OK) return rc;
+        if ((rc = get(pre + "sh_down", PK_Q8, QE_SH_DN_BYTES, 1, &dn)) != QE_OK) return rc;
+        if ((rc = get(pre + "experts", PK_NL4, QE_LAYER_EXPERT_BYTES, QE_N_EXPERT, &ex)) != QE_OK) return rc;
+        const QeLayerPtrs L = layer_ptrs(c, l);
+        HIP_TRY(hipMemcpyAsync(c->arena + (size_t)l * QE_LAYER_EXPERT_BYTES, ex, QE_LAYER_EXPERT_BYTES, k, s));
+        HIP_TRY(hipMemcpyAsync((void *)L.post_norm, pn, QE_D * 4, k, s));
+        HIP_TRY(hipMemcpyAsync((void *)L.router, rt, (size_t)QE_N_EXPERT * QE_D * 4, k, s));
+        HIP_TRY(hipMemcpyAsync((void *)(L.router + (size_t)QE_N_EXPERT * QE_D), sg, QE_D * 4, k, s));
+        HIP_TRY(hipMemcpyAsync((void *)L.sh_gu, gp, QE_SH_GU_BYTES / 2, k, s));
+        HIP_TRY(hipMemcpyAsync((void *)(L.sh_gu + QE_SH_GU_BYTES / 2), up, QE_SH_GU_BYTES / 2, k, s));
+        HIP_TRY(hipMemcpyAsync((void *)L.sh_dn, dn, QE_SH_DN_BYTES, k, s));
+        c->has_bias[l] = 0;
+        HIP_TRY(hipMemcpyAsync(c->bias_on + l, &c->has_bias[l], 1, hipMemcpyHostToDevice, s));
+        HIP_TRY(hipStreamSynchronize(s)); // the mapping goes away with this call
+        c->ready[l] = 1;
+    }
     return QE_OK;
 }
 

@@ -76,6 +76,7 @@ def load(path: str = LIB_PATH):
         "qe_moe_get_logits": (i32, [vp, i32, vp, vp]),
         "qe_moe_dispatch": (i32, [vp, vp, i32, vp]),
         "qe_moe_arena_ptr": (i32, [vp, i32, ctypes.POINTER(vp)]),
+        "qe_moe_load_pack": (i32, [vp, ctypes.c_char_p, i32, i32, i32, vp]),
         "qe_moe_synth_layer": (i32, [vp, i32, u64, vp, vp]),
         "qe_moe_synth_x": (i32, [u64, i32, vp, i64, vp]),
         "qe_moe_last_error": (ctypes.c_char_p, []),
@@ -150,6 +151,9 @@ class MoE:
                   stream=None):
         _check(_lib.qe_moe_set_dense(self.h, layer, _ptr(post_norm), _ptr(router), _ptr(bias), _ptr(sh_gu),
                                      _ptr(sh_down), int(on_device), _stream(stream)))
+
+    def load_pack(self, path, pack_first, first_layer, n_layers, stream=None):
+        _check(_lib.qe_moe_load_pack(self.h, str(path).encode(), pack_first, first_layer, n_layers, _stream(stream)))
 
     def arena_ptr(self, layer) -> int:
         p = ctypes.c_void_p()

@@ -201,6 +201,57 @@ def test_topk_ties_on_gpu(ctx, torch_cuda, kind, T):
     ctx.synth_layer(1, SEED, None)  # restore the synthetic router for later tests
 
 
+class PackLayer:
+    """Oracle view of a layer loaded from a pack (same bytes the loader uploads)."""
+
+    def __init__(self, t):
+        self.router = np.ascontiguousarray(np.vstack([t["router"], t["sh_gate"][None]]), np.float32)
+        self.sh_gu = np.ascontiguousarray(np.concatenate([t["sh_gate_proj"].reshape(-1), t["sh_up"].reshape(-1)]))
+        self.sh_dn = np.ascontiguousarray(t["sh_down"].reshape(-1))
+        self.bias = None
+        self._ex = t["experts"]
+
+    def experts(self, ids):
+        return {int(e): np.ascontiguousarray(self._ex[int(e)]) for e in np.unique(ids)}
+
+
+def test_pack_loader(ctx, torch_cuda, tmp_path):
+    import packfile as PF
+    say("weight pack: blk.3 of a synthetic pack -> context layer 1, norm + residual")
+    t = PF.synth_moe_tensors(1234)
+    path = tmp_path / "moe.pack"
+    PF.write_pack(path, PF.pack_entries(3, t))
+    ctx.load_pack(path, 3, 1, 1)
+    L = PackLayer(t)
+    for T in (1, 20):
+        x = O.gen_x(SEED, 500 + T, T)
+        xd = torch_cuda.from_numpy(x).cuda()
+        y = torch_cuda.empty_like(xd)
+        ctx.forward(1, xd, y, T)
+        torch_cuda.cuda.synchronize()
+        g = ctx.routing(T)
+        o = O.moe_layer(L, x, norm=True, residual=True, post_norm=t["post_norm"])
+        assert np.array_equal(ctx.logits(T).view(np.uint32), o["logits"].view(np.uint32)), "router logits differ"
+        assert np.array_equal(g["ids"], o["ids"])
+        e_out, e_sd = rel_l2(y.cpu().numpy(), o["out"]), rel_l2(g["sd"], o["sd"])
+        say(f"  T={T} out rel-L2 {e_out:.2e}  shared rel-L2 {e_sd:.2e}")
+        assert e_out <= TOL and e_sd <= TOL
+    # errors come back as codes with a message, nothing is half-loaded into a ready layer
+    bad = tmp_path / "bad.pack"
+    PF.write_pack(bad, PF.pack_entries(3, t), magic=b"NOTAPACK")
+    with pytest.raises(qe_moe.QeError, match="bad magic"):
+        ctx.load_pack(bad, 3, 1, 1)
+    with pytest.raises(qe_moe.QeError, match="missing blk.4.post_norm"):
+        ctx.load_pack(path, 4, 1, 1)
+    PF.write_pack(bad, PF.pack_entries(3, t, {"sh_up": PF.F_Q6}))
+    with pytest.raises(qe_moe.QeError, match="sh_up has format 2"):
+        ctx.load_pack(bad, 3, 1, 1)
+    with pytest.raises(qe_moe.QeError, match="cannot open"):
+        ctx.load_pack(tmp_path / "none.pack", 3, 1, 1)
+    _layers.pop((1, None), None)
+    ctx.synth_layer(1, SEED, None)
+
+
 def test_dispatch_on_reference_routing_records(ctx, torch_cuda):
     import os
     torch = torch_cuda
