@@ -7,11 +7,14 @@ x_{l+1} = x_l + MoE_l(RMSNorm(x_l)), all 40 x 256 experts resident in one
 HBM arena, inputs resident in HBM before timing.  Also reported:
   * hbm_gbs: algorithmic bytes/token (40 x 19,619,840 B) x tokens/s;
   * prefill512_tflops: BASELINE config 3 (512 tokens, one layer, Zipf s=1
-    router bias), 29.53 GFLOP per call / time;
-  * roofline: the dominant decode kernel (routed gate/up, k_gu) timed with HIP
-    events on its own stream over a profiled pass of the same workload;
+    router bias), 29.53 GFLOP per call / time, with its roofline (AI x HBM
+    peak vs the fp16 MFMA peak) and the routed grouped-GEMM rate alone;
+  * roofline: the decode kernel (k_decode, the only kernel of a decode step)
+    timed with the library's HIP events on the launch stream over a profiled
+    pass of the same workload;
   * cpu_baseline: the CPU AVX2 restatement of the reference CPU MoE path
-    (oracle/qe_oracle.cpp) on a bounded sample, host cores, same process.
+    (oracle/qe_oracle.cpp) on a bounded sample, host cores, same process, at
+    the box's thread share and at the reference's default of 12 threads.
 Weights are random-init from the seeded generator (no checkpoints offline).
 """
 import argparse
@@ -32,6 +35,10 @@ LAYER_BYTES_B1 = 8 * EXPERT_BYTES + 1024 * 2176 + 2048 * 544 + 257 * 2048 * 4 + 
 N_LAYERS = 40
 FLOP_PER_TOKEN = 8 * 6291456 + 6291456 + 2 * 257 * 2048  # 57,675,776
 HBM_PEAK = 8.0e12
+FP16_PEAK = 2.5e15
+INT8_PEAK = 5.0e15
+DENSE_BYTES = 1024 * 2176 + 2048 * 544 + 257 * 2048 * 4 + 2048 * 4  # shared Q8, router, post_norm
+ROUTED_FLOP_PER_PAIR = 2 * 1024 * 2048 + 2 * 2048 * 512  # gate/up + down of one (token, expert) pair
 SEED = 0x51E3_6B50
 TRAFFIC_FILE = "profiles/k_decode_cfg2_pmc.txt"
 
@@ -228,7 +235,24 @@ def main():
         mp.profile(False)
         r = mp.routing(512)
         cnt = np.diff(r["off"])
-        pre = {"prefill512_ms": round(pms, 4), "prefill512_tflops": round(512 * FLOP_PER_TOKEN / (pms / 1e3) / 1e12, 3),
+        flop = 512 * FLOP_PER_TOKEN
+        pbytes = int(np.count_nonzero(cnt)) * EXPERT_BYTES + DENSE_BYTES + 2 * 512 * 2048 * 4
+        ai = flop / pbytes
+        ceiling = min(FP16_PEAK, ai * HBM_PEAK)
+        achieved_p = flop / (pms / 1e3)
+        gkey = [k for k in pk if k.startswith("k_expert_gu")][0]
+        g_s = pk[gkey][0] / pk[gkey][1] / 1e3
+        routed_flop = 512 * 8 * ROUTED_FLOP_PER_PAIR
+        pre = {"prefill512_ms": round(pms, 4), "prefill512_tflops": round(achieved_p / 1e12, 3),
+               "prefill512_roofline": {"bound": "hbm" if ai * HBM_PEAK < FP16_PEAK else "mfma",
+                                       "algorithmic_bytes": pbytes, "flop": flop, "ai_flop_per_byte": round(ai, 1),
+                                       "ceiling_tflops": round(ceiling / 1e12, 1),
+                                       "frac": round(achieved_p / ceiling, 4)},
+               "prefill512_routed_gemm": {"kernels": gkey, "us": round(g_s * 1e6, 2), "flop": routed_flop,
+                                          "tops": round(routed_flop / g_s / 1e12, 2), "mfma": "i32_16x16x32_i8",
+                                          "frac_int8_peak": round(routed_flop / g_s / INT8_PEAK, 4),
+                                          "frac_fp16_peak": round(routed_flop / g_s / FP16_PEAK, 4),
+                                          "note": "time includes the shared-expert down tiles (1.07 GFLOP) of the same launch"},
                "prefill512_routing": {"distinct_experts": int(np.count_nonzero(cnt)), "max_tokens_per_expert": int(cnt.max()),
                                       "top8_share": round(float(np.sort(cnt)[-8:].sum() / cnt.sum()), 4),
                                       "experts_lt4_tokens": int(((cnt > 0) & (cnt < 4)).sum())},
@@ -245,6 +269,13 @@ def main():
                "sample": f"{cpu_tok} tokens of B=1 decode through the 40-step stack ({args.cpu_layers} distinct seeded "
                          f"layers with all 256 experts each, cycled), full layer per step: norm, router, top-8, "
                          f"dispatch, int8 experts, Q8 shared, combine, residual; {cpu_sec:.2f} s of timed CPU work"}
+        if threads != 12:  # the reference's default pool size (engine/qe.cpp:1201)
+            t12, s12, n12 = cpu_baseline(args.cpu_layers, args.cpu_seconds / 2, 100000, 12)
+            cpu["threads_12"] = {"value": round(t12, 3), "tokens": n12, "seconds": round(s12, 2)}
+        try:
+            cpu["cpu_model"] = [l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo") if l.startswith("model name")][0]
+        except (OSError, IndexError):
+            pass
 
     traffic = pmc_traffic(os.path.join(REPO, TRAFFIC_FILE))
     out = {
