@@ -288,12 +288,9 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
                 __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)(pnorm + i * 64 + lane),
                                                  (__attribute__((address_space(3))) void *)(s_pn + i * 65), 4, 0, 0);
         }
-        if (li > 0) { // x: one word per (8-row group, token) polled first, then all read with tags verified
-            if (tid < T * 256) {
-                uint64_t w[1];
-                poll_tv2<1>(src_x + (tid >> 8) * QE_D + (tid & 255) * 8 + 7, 0, tagIn, w, true, a.err);
-            }
-            __syncthreads();
+        if (li > 0 && tid < T * 256) { // x: one word per (8-row group, token) polled first; the
+            uint64_t w[1];               // rest of the workgroup polls its own words directly
+            poll_tv2<1>(src_x + (tid >> 8) * QE_D + (tid & 255) * 8 + 7, 0, tagIn, w, true, a.err);
         }
         // raw x of all tokens -> LDS (natural layout, token stride 2048; T*2048 is a multiple of 2 NTH)
         if (li == 0) {
