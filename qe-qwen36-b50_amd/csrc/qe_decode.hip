@@ -433,10 +433,43 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
                 for (int j = 0; j < 4; ++j) a.logits[t * QE_ROUTER_ROWS + lane + 64 * j] = v[j];
                 if (lane == 0) a.logits[t * QE_ROUTER_ROWS + QE_N_EXPERT] = v[4];
             }
-            wave_topk_vals(v, v[4], lane, s_ids + t * QE_K_USED, s_wts + t * QE_K_USED, s_shg + t);
+            const int myid = wave_topk_vals(v, v[4], lane, s_ids + t * QE_K_USED, s_wts + t * QE_K_USED, s_shg + t);
+            if (TM == 1) {
+                // one token: its 8 distinct experts are the items, in expert order
+                // (engine/qe.cpp:1965-1976 with one pair per expert): lane k < 8
+                // holds pair k's expert, and its slot is the count of smaller ids
+                int id8[QE_K_USED], rank = 0;
+#pragma unroll
+                for (int j = 0; j < QE_K_USED; ++j) {
+                    id8[j] = __builtin_amdgcn_readlane(myid, j);
+                    rank += id8[j] < myid;
+                }
+                if (lane < QE_K_USED) {
+                    s_pairs[rank] = lane;
+                    s_items[rank] = make_int4(myid, rank, 1, 0);
+                }
+                if (lane == 0) s_misc[0] = QE_K_USED;
+                if (last && blockIdx.x == 0) {
+                    if (lane < QE_K_USED) {
+                        a.pairs[rank] = lane;
+                        a.ids[lane] = myid;
+                        a.wts[lane] = s_wts[lane];
+                    }
+                    if (lane == 0) a.shg[0] = s_shg[0];
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) { // per-expert offsets for the routing sink
+                        const int ee = lane * 4 + k;
+                        int o = 0;
+#pragma unroll
+                        for (int j = 0; j < QE_K_USED; ++j) o += id8[j] < ee;
+                        a.off[ee] = o;
+                    }
+                    if (lane == 0) a.off[QE_N_EXPERT] = QE_K_USED;
+                }
+            }
         }
         __syncthreads();
-        if (wv == 0) {
+        if (TM != 1 && wv == 0) {
             // stable counting sort of the T*8 pairs by expert (engine/qe.cpp:1965-1976):
             // slot of pair p = #pairs with a smaller expert + #earlier pairs with the same one
             const int e = lane < np ? s_ids[lane] : 1 << 20;
@@ -471,7 +504,7 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
                 if (lane == 0) a.off[QE_N_EXPERT] = np;
             }
         }
-        __syncthreads();
+        if (TM != 1) __syncthreads();
         const int nitems = s_misc[0];
 
         // Down rows of this workgroup's first D row group for the first DEC_PFI
