@@ -1,18 +1,18 @@
-// Prefill expert products as MFMA grouped GEMMs (Engine::moe_round_xmx and
-// moe_xmx, engine/qe.cpp:2103-2154 and :369-436, redesigned for CDNA4).
+// Prefill (T > 8) matrix-core kernels: the routed experts as int8 MFMA grouped
+// GEMMs (Engine::moe_round_xmx and moe_xmx, engine/qe.cpp:2103-2154 and
+// :369-436, redesigned for CDNA4), the router tiles and the Q8 shared expert.
 //
 // Exactness: the reference CPU path multiplies int8 activations by IQ4_NL
 // codebook values exactly per 32-block and applies fp32 block scales after
-// (engine/qe.cpp:704-741).  Both operands are small integers (|v| <= 127),
-// exact in fp16, so v_mfma_f32_32x32x16_f16 on them returns the exact integer
-// block dot in fp32; two MFMAs cover one 32-block.  The fp32 epilogue then
-// applies xs[m][b] * dw[n][b] per block, so results agree with the CPU path
-// to fp32 rounding.  (Scaled fp16/bf16 operands would not: the h quantisation
-// downstream turns 1e-4 relative noise into >1e-3 output error.)
+// (engine/qe.cpp:704-741).  v_mfma_i32_16x16x32_i8 consumes one 32-element
+// block per instruction, so every block dot is an exact int32, and the fp32
+// epilogue applies xs[m][b] * dw[n][b] per block: results agree with the CPU
+// path to fp32 rounding.  (Scaled fp16/bf16 operands would not: the h
+// quantisation downstream turns 1e-4 relative noise into >1e-3 output error.)
 //
-// Work item: (expert e, up to 128 of its pairs in dispatch order) x N-tile.
+// Work item: (expert e, up to 32 of its pairs in dispatch order) x row group.
 //   gate/up epilogue: h = silu(g)*u, quantised per 32-block (the quant_x step
-//   of engine/qe.cpp:2078-2081), stored as fp16 integers + fp32 scales;
+//   of engine/qe.cpp:2078-2081), stored int8 in the operand layout + fp32 scales;
 //   down epilogue: yp[p][n] = w_p * y.
 #include "qe_kernels.h"
 
@@ -74,9 +74,9 @@ struct GemmTileArgs {
 // so it is issued 8 blocks ahead of its use into the slot's own registers.
 // Block scales of the wave's rows are staged once in LDS.
 //   gate/up: groups = gate j0..j0+15, j0+16..j0+31, up j0.., up j0+16.. with
-//            j0 = 32 (4 blockIdx.y + wave): h and its 32-block quantisation
-//            stay inside the wave.
-//   down:    groups = output rows 256 blockIdx.y + 64 wave + 16 c + 0..15.
+//            j0 = 32 (4 yb + wave) for row group yb: h and its 32-block
+//            quantisation stay inside the wave.
+//   down:    groups = output rows 256 yb + 64 wave + 16 c + 0..15.
 typedef unsigned qe_u32x2 __attribute__((ext_vector_type(2)));
 typedef unsigned qe_u32x4 __attribute__((ext_vector_type(4)));
 
