@@ -207,6 +207,17 @@ def main():
     dec_bytes = N_LAYERS * LAYER_BYTES_B1  # one launch = one token through all 40 layers
     achieved = dec_bytes / dec_avg_s
     kernels = {k: {"avg_us": round(v[0] / v[1] * 1e3, 3), "launches": v[1]} for k, v in prof.items()}
+
+    # batched decode, 8 tokens per step through the same 40 layers (the T <= 8 kernel)
+    x8 = torch.empty(8, 2048, device=dev)
+    qe_moe.synth_x(SEED, 1, x8, x8.numel(), stream=stream)
+    y8 = torch.empty_like(x8)
+    step8 = lambda: m.forward_stack(0, N_LAYERS, x8, y8, 8, stream=torch.cuda.current_stream())  # noqa: E731
+    for _ in range(5):
+        step8()
+    ms8 = timed(torch, step8, max(20, args.steps // 4), torch.cuda.current_stream())
+    decode_b8 = {"tokens_per_s": round(8000.0 / ms8, 1), "ms_per_step": round(ms8, 4),
+                 "note": "8 tokens per step through the 40-layer stack, no bias (independent tokens)"}
     del m
     torch.cuda.empty_cache()
 
@@ -294,6 +305,7 @@ def main():
                      "bytes_per_launch": dec_bytes,
                      "avg_us": round(dec_avg_s * 1e6, 3)},
         "kernels": kernels,
+        "decode_b8": decode_b8,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

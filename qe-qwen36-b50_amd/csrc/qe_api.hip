@@ -98,7 +98,7 @@ int qe_moe_create(int device, int n_layers, int t_max, qe_moe_ctx **out) {
     c->has_bias.assign(n_layers, 0);
     c->ready.assign(n_layers, 0);
     const size_t L = (size_t)n_layers, T = (size_t)t_max, NP = T * QE_K_USED, T32 = (T + 31) & ~(size_t)31;
-    const size_t max_items = NP / QE_MFMA_MC + QE_N_EXPERT;
+    const size_t max_items = NP / (QE_MFMA_MC / 2 + 1) + 1 + QE_N_EXPERT; // big items hold > MC / 2 pairs
     const size_t nch = (NP + 1023) / 1024;
     int rc = QE_OK;
     QeScratch &S = c->S;

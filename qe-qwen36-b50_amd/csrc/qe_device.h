@@ -21,11 +21,19 @@ QE_DEV uint32_t nl4_lookup4(uint32_t idx /* 4 indices, one per byte, 0..15 */) {
     const uint32_t sel = ((idx >> 1) & 0x04040404u) | 0x03020100u;     // bit 3 -> take b
     return __builtin_amdgcn_perm(b, a, sel);
 }
+// (v & 0x04040404) | 0x03020100 in one v_and_or_b32.  GFX9 VOP3 takes no
+// literal and one SGPR, so the mask rides in an SGPR and the byte ramp in a
+// VGPR (both loop-invariant); plain C gets an and plus an or.
+QE_DEV uint32_t nl4_merge_sel(uint32_t v) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(v), "s"(0x04040404u), "v"(0x03020100u));
+    return r;
+}
 // Both nibbles of 4 code bytes; the bit-3 selector comes straight from the
 // code bytes (bits 3 and 7), without extracting the nibbles first.
 QE_DEV void nl4_decode_dword(uint32_t q, uint32_t &lo, uint32_t &hi) {
     const uint32_t il = q & 0x07070707u, ih = (q >> 4) & 0x07070707u;
-    const uint32_t sl = ((q >> 1) & 0x04040404u) | 0x03020100u, sh = ((q >> 5) & 0x04040404u) | 0x03020100u;
+    const uint32_t sl = nl4_merge_sel(q >> 1), sh = nl4_merge_sel(q >> 5);
     lo = __builtin_amdgcn_perm(__builtin_amdgcn_perm(QE_NL4_W3, QE_NL4_W2, il), __builtin_amdgcn_perm(QE_NL4_W1, QE_NL4_W0, il), sl);
     hi = __builtin_amdgcn_perm(__builtin_amdgcn_perm(QE_NL4_W3, QE_NL4_W2, ih), __builtin_amdgcn_perm(QE_NL4_W1, QE_NL4_W0, ih), sh);
 }

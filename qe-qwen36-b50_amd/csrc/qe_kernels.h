@@ -7,7 +7,7 @@
 
 #define QE_SMALL_T 8   /* calls of up to this many tokens take the persistent decode kernel */
 #define RT_SPLIT 8     /* router K split: subtrees of 64 / RT_SPLIT chunks, merged by k_topk */
-#define QE_MFMA_MC 32 /* pairs per work item of the prefill MFMA grouped GEMMs (up to two 16-row tiles) */
+#define QE_MFMA_MC 64 /* pairs per work item of the prefill MFMA grouped GEMMs (up to four 16-row tiles) */
 
 
 // One layer's weights inside the context.

@@ -64,19 +64,19 @@ struct GemmTileArgs {
 // 4g..4g+3, so a lane's B operand is one dword of codes and its A operand one
 // 8-byte run of the operand layout.
 //
-// Wave = 64 weight rows (4 column groups of 16) x the item's <= 32 pairs (NT
-// 16-row tiles), streaming K.  Codes arrive 16 bytes per lane: lane (n, g) loads
+// Wave = 16 NC weight rows (NC column groups of 16) x NT 16-pair tiles, streaming
+// K in turns of 8 blocks.  Codes arrive 16 bytes per lane: lane (n, g) loads
 // block 4Q+g of its row, four 16-lane rows of the wave cover a quad of blocks,
 // and a 4x4 transpose over the rows (v_permlane32_swap, v_permlane16_swap)
-// hands lane (n, g) dword g of each block of the quad.  The load ring holds two
+// hands lane (n, g) dword g of each block of the quad.  The code ring holds two
 // quads; loads are never predicated (the last refills wrap to the first blocks)
 // and each refill takes an offset that depends on the last read of its slot,
 // so it is issued 8 blocks ahead of its use into the slot's own registers.
-// Block scales of the wave's rows are staged once in LDS.
-//   gate/up: groups = gate j0..j0+15, j0+16..j0+31, up j0.., up j0+16.. with
-//            j0 = 32 (4 yb + wave) for row group yb: h and its 32-block
-//            quantisation stay inside the wave.
-//   down:    groups = output rows 256 yb + 64 wave + 16 c + 0..15.
+// The four waves of a workgroup share the item's pairs: each turn's activations
+// (256 bytes of K per pair) and block scales, and the weight scales of the
+// workgroup's rows, are loaded once per workgroup into a double-buffered LDS
+// stage (issued a turn ahead, stored and published by one barrier at the end of
+// the turn), and every wave reads its A operands from there.
 typedef unsigned qe_u32x2 __attribute__((ext_vector_type(2)));
 typedef unsigned qe_u32x4 __attribute__((ext_vector_type(4)));
 
@@ -89,123 +89,161 @@ QE_DEV void transpose_rows4(uint32_t d[4]) {
     d[0] = u.x; d[1] = u.y; d[2] = v.x; d[3] = v.y;
 }
 
-template <bool GU> struct ExpertSmem {
+// LDS of one (NC, NT) tile, in bytes from the start of ExpertSmem::raw:
+//   weight scales of the workgroup's rows, whole K: fp16 [block][wave][n][group];
+//   two stages of the item's activations for one turn: [pair][256 bytes], the
+//     16-byte chunk q of pair m stored at chunk q ^ (m % 16) -- the sixteen rows a
+//     lane group reads in one instruction fall in sixteen different bank groups;
+//   two stages of their block scales for the turn: fp32 [block of the turn][pair].
+template <bool GU, int NC, int NT> struct TileLds {
     static constexpr int NB = (GU ? QE_D : QE_FF_EXP) / 32;
-    float xs[QE_MFMA_MC / 16][NB][16]; // activation scale per (tile, block, row)
-    uint16_t dw[4][NB][16][4];         // fp16 weight scale per (wave, block, n, group)
+    static constexpr int DW = 0, DW_SZ = NB * 4 * 16 * NC * 2;
+    static constexpr int ACT = DW + DW_SZ, ACT_SZ = 16 * NT * 256;
+    static constexpr int XS = ACT + 2 * ACT_SZ, XS_SZ = 8 * 16 * NT * 4;
+    static constexpr int SIZE = XS + 2 * XS_SZ;
+};
+constexpr int qe_cmax(int a, int b) { return a > b ? a : b; }
+template <bool GU> struct ExpertSmem {
+    static constexpr int SIZE = qe_cmax(TileLds<GU, 2, 4>::SIZE, qe_cmax(TileLds<GU, 2, 2>::SIZE, TileLds<GU, 2, 1>::SIZE));
+    alignas(16) uint8_t raw[SIZE];
     int pair[QE_MFMA_MC];
+    float amax[GU ? 4 : 1][QE_MFMA_MC]; // gate/up with NC = 2: each wave's |h| maximum per pair
 };
 
-template <bool GU, int NT>
+// Wave = NC column groups of 16 weight rows x NT 16-pair tiles (NC MFMAs per
+// block and tile; each weight decoded once per item).
+// Row groups yb of a workgroup (4 waves):
+//   gate/up, NC = 4: h rows 32 (4 yb + wave) + 0..31; groups gate, gate+16, up, up+16;
+//   gate/up, NC = 2: h rows 16 (4 yb + wave) + 0..15; groups gate, up -- a 32-block
+//            of h spans the wave pair (2w, 2w+1), which meets in LDS for its maximum;
+//   down:    output rows 64 NC yb + 16 NC wave + 16 c + 0..15.
+template <bool GU, int NC, int NT>
 __device__ __forceinline__ void expert_tile(const GemmTileArgs &a, const int4 it, const int yb, ExpertSmem<GU> &sm) {
+    static_assert(NC == 2 || NC == 4, "two or four column groups per wave");
+    static_assert(16 * NT <= QE_MFMA_MC, "tiles of the item");
     constexpr int KD = GU ? QE_D : QE_FF_EXP;  // reduction length
     constexpr int NB = KD / 32;                // K blocks
-    constexpr int NCH = NB / 8;                // ring turns (two quads each)
+    constexpr int NCH = NB / 8;                // turns (two quads each)
     constexpr uint32_t RB = GU ? QE_GU_ROW_BYTES : QE_DN_ROW_BYTES;
-    auto &s_xs = sm.xs;
-    auto &s_dw = sm.dw;
     auto &s_pair = sm.pair;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, n = lane & 15, g = lane >> 4;
-    auto row_of = [&](int w, int c, int nn) {
-        return GU ? (c < 2 ? 0 : QE_FF_EXP) + (yb * 4 + w) * 32 + 16 * (c & 1) + nn : yb * 256 + w * 64 + 16 * c + nn;
+    auto row_of = [&](int w, int c, int nn) -> int {
+        if constexpr (!GU) return yb * (64 * NC) + w * (16 * NC) + 16 * c + nn;
+        else if constexpr (NC == 4) return (c < 2 ? 0 : QE_FF_EXP) + (yb * 4 + w) * 32 + 16 * (c & 1) + nn;
+        else return (c == 0 ? 0 : QE_FF_EXP) + (yb * 4 + w) * 16 + nn;
     };
     const uint8_t *ebase = a.arena + (size_t)it.x * QE_EXPERT_BYTES + (GU ? 0 : QE_EXPERT_DOWN_OFF);
-    {
-        // thread = one weight row of the workgroup: its NB scales -> s_dw
-        const int c = (tid >> 4) & 3;
-        const uint4 *sc = (const uint4 *)(ebase + (size_t)row_of(wv, c, n) * RB + KD / 2);
-        uint4 v[NB / 8];
-#pragma unroll
-        for (int i = 0; i < NB / 8; ++i) v[i] = sc[i];
-#pragma unroll
-        for (int i = 0; i < NB / 8; ++i) {
-            const uint32_t w4[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
-#pragma unroll
-            for (int j = 0; j < 8; ++j) s_dw[wv][8 * i + j][n][c] = (uint16_t)(w4[j >> 1] >> (16 * (j & 1)));
-        }
-    }
-    if (tid < QE_MFMA_MC) s_pair[tid] = tid < it.z ? a.pairs[it.y + tid] : -1;
-    __syncthreads();
-    {
-        constexpr int NV = 16 * NT * NB / 256; // scales of the item's NT tiles, per thread
-        float v[NV];
-#pragma unroll
-        for (int k = 0; k < NV; ++k) {
-            const int i = tid + 256 * k, m = i / NB, b = i % NB, p = s_pair[m];
-            v[k] = p < 0 ? 0.f : a.as[(size_t)(p / a.a_row_div) * NB + b];
-        }
-#pragma unroll
-        for (int k = 0; k < NV; ++k) {
-            const int i = tid + 256 * k, m = i / NB, b = i % NB;
-            s_xs[m >> 4][b][m & 15] = v[k];
-        }
-    }
-    __syncthreads();
-
     // Buffer loads: a range-checked resource per operand (reads past the end
     // return 0), uniform per-turn offsets in SGPRs, per-lane offsets fixed.
     const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
         (void *)ebase, (short)0, (int)(GU ? QE_EXPERT_DOWN_OFF : QE_EXPERT_BYTES - QE_EXPERT_DOWN_OFF), 0x00020000);
     const __amdgpu_buffer_rsrc_t ar = __builtin_amdgcn_make_buffer_rsrc((void *)a.aq, (short)0, a.a_bytes, 0x00020000);
-    int rowc[4];
-    uint32_t boff[4]; // byte offset of block g of the lane's row, per column group
+    auto ld128 = [](__amdgpu_buffer_rsrc_t r, uint32_t vo, int so) {
+        const qe_u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, vo, so, 0);
+        return make_uint4(v.x, v.y, v.z, v.w);
+    };
+    using LY = TileLds<GU, NC, NT>;
+    uint8_t *const lds = sm.raw;
+
+    int rowc[NC];
+    uint32_t boff[NC]; // byte offset of block g of the lane's row, per column group
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
+    for (int c = 0; c < NC; ++c) {
         rowc[c] = row_of(wv, c, n);
         boff[c] = (uint32_t)rowc[c] * RB + 16 * g;
     }
-    uint32_t aoff[NT];
+    // Ring: quad slot qs of turn ch holds blocks 8 ch + 4 qs .. +3; refills wrap
+    // to turn (ch + 1) % NCH.
+    uint4 rq[2][NC]; // raw codes, per quad slot and column group
+    auto load_q = [&](int ch, int qs, uint32_t dep) {
 #pragma unroll
-    for (int t = 0; t < NT; ++t) {
-        const int p = s_pair[16 * t + n];
-        aoff[t] = (uint32_t)((p < 0 ? s_pair[0] : p) / a.a_row_div) * KD + 16 * g; // padding rows: scale 0
-    }
+        for (int c = 0; c < NC; ++c) rq[qs][c] = ld128(wr, boff[c] + dep, 128 * ch + 64 * qs);
+    };
 
-    float acc[4][NT][4];
+    // Start-up: the loads that depend on the expert only (turn 0 of the code
+    // ring, the weight scales) go out before the pairs, which gate the activations.
+    load_q(0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    load_q(0, 1, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    static_assert(64 * NC <= 256, "one weight row per thread");
+    const bool dw_role = tid < 64 * NC; // thread = one weight row of the workgroup: its NB scales
+    const int dw_w = tid / (16 * NC), dw_c = (tid >> 4) % NC, dw_n = tid & 15;
+    uint4 dwv[NB / 8];
+    if (dw_role) {
+        const uint4 *sc = (const uint4 *)(ebase + (size_t)row_of(dw_w, dw_c, dw_n) * RB + KD / 2);
 #pragma unroll
-    for (int c = 0; c < 4; ++c)
+        for (int i = 0; i < NB / 8; ++i) dwv[i] = sc[i];
+    }
+    if (tid < QE_MFMA_MC) s_pair[tid] = tid < it.z ? a.pairs[it.y + tid] : -1;
+    __syncthreads();
+
+    // Stage roles of this thread, per turn:
+    //   activations: pair m = 16 r + tid / 16, chunk q = tid % 16 of the turn, r < NT
+    //     (padding pairs load pair 0's row; their scales are 0);
+    //   activation scales (tid >= 256 - 32 NT): blocks 4 h .. 4 h + 3 of the turn of pair m.
+    uint32_t act_off[NT];
+#pragma unroll
+    for (int r = 0; r < NT; ++r) {
+        const int p = s_pair[16 * r + (tid >> 4)];
+        act_off[r] = (uint32_t)((p < 0 ? s_pair[0] : p) / a.a_row_div) * KD + 16 * (tid & 15);
+    }
+    const int act_st = (tid >> 4) * 256 + (((tid & 15) ^ ((tid >> 4) & 15)) << 4); // + 16 r * 256
+    const int xs_i = tid - (256 - 32 * NT), xs_m = xs_i >> 1, xs_h = xs_i & 1;
+    const bool xs_role = xs_i >= 0;
+    const int xs_p = xs_role ? s_pair[xs_m] : -1;
+    const float4 *xs_src = (const float4 *)(a.as + (size_t)((xs_p < 0 ? 0 : xs_p) / a.a_row_div) * NB + 4 * xs_h);
+    uint4 sa[NT];
+    float4 sxs = make_float4(0.f, 0.f, 0.f, 0.f);
+    auto stage_load = [&](int ch) {
+#pragma unroll
+        for (int r = 0; r < NT; ++r) sa[r] = ld128(ar, act_off[r], 256 * ch);
+        if (xs_p >= 0) sxs = xs_src[2 * ch];
+    };
+    auto stage_store = [&](int s) {
+        uint8_t *act = lds + LY::ACT + s * LY::ACT_SZ;
+#pragma unroll
+        for (int r = 0; r < NT; ++r) *(uint4 *)(act + 16 * r * 256 + act_st) = sa[r];
+        if (xs_role) {
+            float *xs = (float *)(lds + LY::XS + s * LY::XS_SZ) + xs_m;
+            xs[(4 * xs_h + 0) * 16 * NT] = sxs.x;
+            xs[(4 * xs_h + 1) * 16 * NT] = sxs.y;
+            xs[(4 * xs_h + 2) * 16 * NT] = sxs.z;
+            xs[(4 * xs_h + 3) * 16 * NT] = sxs.w;
+        }
+    };
+    stage_load(0);
+    if (dw_role) {
+        uint16_t *dwl = (uint16_t *)(lds + LY::DW) + (dw_w * 16 + dw_n) * NC + dw_c;
+#pragma unroll
+        for (int i = 0; i < NB / 8; ++i) {
+            const uint32_t w4[4] = {dwv[i].x, dwv[i].y, dwv[i].z, dwv[i].w};
+#pragma unroll
+            for (int j = 0; j < 8; ++j) dwl[(8 * i + j) * 64 * NC] = (uint16_t)(w4[j >> 1] >> (16 * (j & 1)));
+        }
+    }
+    stage_store(0);
+    __syncthreads();
+
+    float acc[NC][NT][4];
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
 #pragma unroll
         for (int t = 0; t < NT; ++t)
 #pragma unroll
             for (int i = 0; i < 4; ++i) acc[c][t][i] = 0.f;
 
-    // Ring: quad slot qs of turn ch holds blocks 8 ch + 4 qs .. +3; pair slot
-    // ps holds blocks 8 ch + 2 ps, +1.  Refills wrap to turn (ch + 1) % NCH.
-    uint4 rq[2][4];      // raw codes, per quad slot and column group
-    uint4 ra[4][NT];     // activations, per pair slot and tile
-    auto ld128 = [](__amdgpu_buffer_rsrc_t r, uint32_t vo, int so) {
-        const qe_u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, vo, so, 0);
-        return make_uint4(v.x, v.y, v.z, v.w);
-    };
-    auto load_q = [&](int ch, int qs, uint32_t dep) {
-#pragma unroll
-        for (int c = 0; c < 4; ++c) rq[qs][c] = ld128(wr, boff[c] + dep, 128 * ch + 64 * qs);
-    };
-    auto load_a = [&](int ch, int ps, uint32_t dep) {
-#pragma unroll
-        for (int t = 0; t < NT; ++t) ra[ps][t] = ld128(ar, aoff[t] + dep, 256 * ch + 64 * ps);
-    };
-    // same issue order as the refills, so the loop's wait counts hold on entry
-    load_q(0, 0, 0);
-    __builtin_amdgcn_sched_barrier(0);
-    load_a(0, 0, 0);
-    __builtin_amdgcn_sched_barrier(0);
-    load_a(0, 1, 0);
-    __builtin_amdgcn_sched_barrier(0);
-    load_q(0, 1, 0);
-    __builtin_amdgcn_sched_barrier(0);
-    load_a(0, 2, 0);
-    __builtin_amdgcn_sched_barrier(0);
-    load_a(0, 3, 0);
-    __builtin_amdgcn_sched_barrier(0);
-
     for (int ch = 0; ch < NCH; ++ch) {
         const int nx = ch + 1 < NCH ? ch + 1 : 0;
+        const uint8_t *act = lds + LY::ACT + (ch & 1) * LY::ACT_SZ;
+        const float *xsl = (const float *)(lds + LY::XS + (ch & 1) * LY::XS_SZ);
+        if (ch + 1 < NCH) stage_load(ch + 1); // next turn's stage, a turn ahead
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int qs = 0; qs < 2; ++qs) {
-            uint32_t cw[4][4]; // [group][block of the quad]: the lane's code dword
+            uint32_t cw[NC][4]; // [group][block of the quad]: the lane's code dword
 #pragma unroll
-            for (int c = 0; c < 4; ++c) {
+            for (int c = 0; c < NC; ++c) {
                 // copy out of the ring first: the swaps overwrite their operands, and
                 // the ring registers must stay free for the refill
                 const uint32_t r4[4] = {rq[qs][c].x, rq[qs][c].y, rq[qs][c].z, rq[qs][c].w};
@@ -215,68 +253,76 @@ __device__ __forceinline__ void expert_tile(const GemmTileArgs &a, const int4 it
             }
             {
                 uint32_t dep;
-                asm volatile("v_mov_b32 %0, 0" : "=v"(dep)
-                             : "v"(cw[0][0]), "v"(cw[1][0]), "v"(cw[2][0]), "v"(cw[3][0]));
+                if constexpr (NC == 4)
+                    asm volatile("v_mov_b32 %0, 0" : "=v"(dep)
+                                 : "v"(cw[0][0]), "v"(cw[1][0]), "v"(cw[2][0]), "v"(cw[3][0]));
+                else
+                    asm volatile("v_mov_b32 %0, 0" : "=v"(dep) : "v"(cw[0][0]), "v"(cw[1][0]));
                 load_q(nx, qs, dep);
                 __builtin_amdgcn_sched_barrier(0);
             }
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int s = 4 * qs + j, b = 8 * ch + s, ps = s >> 1;
-                long bv[4];
+            for (int jp = 0; jp < 2; ++jp) {
+                // pair slot: blocks 4 qs + 2 jp, +1 of the turn; one 16-byte LDS read per tile
+                const int ps = 2 * qs + jp;
+                uint4 av2[NT];
 #pragma unroll
-                for (int c = 0; c < 4; ++c) {
-                    uint32_t lo, hi;
-                    nl4_decode_dword(cw[c][j], lo, hi);
-                    bv[c] = (long)(((uint64_t)hi << 32) | lo);
-                }
-                const uint2 d2 = *(const uint2 *)&s_dw[wv][b][n][0];
-                float dw[4];
-                dw[0] = f16_bits_to_f32((uint16_t)(d2.x & 0xffffu));
-                dw[1] = f16_bits_to_f32((uint16_t)(d2.x >> 16));
-                dw[2] = f16_bits_to_f32((uint16_t)(d2.y & 0xffffu));
-                dw[3] = f16_bits_to_f32((uint16_t)(d2.y >> 16));
-                // per tile: four exact block dots on the matrix cores, then the fp32 scaling
+                for (int t = 0; t < NT; ++t) av2[t] = *(const uint4 *)(act + (16 * t + n) * 256 + (((4 * ps + g) ^ n) << 4));
 #pragma unroll
-                for (int t = 0; t < NT; ++t) {
-                    const uint4 v = ra[ps][t];
-                    const long av = (s & 1) ? (long)(((uint64_t)v.w << 32) | v.z) : (long)(((uint64_t)v.y << 32) | v.x);
-                    typedef int i32x4 __attribute__((ext_vector_type(4)));
-                    i32x4 P[4];
+                for (int jj = 0; jj < 2; ++jj) {
+                    const int j = 2 * jp + jj, s = 4 * qs + j; // block s of the turn
+                    long bv[NC];
 #pragma unroll
-                    for (int c = 0; c < 4; ++c) {
-                        const i32x4 zero = {0, 0, 0, 0};
-                        P[c] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bv[c], zero, 0, 0, 0);
+                    for (int c = 0; c < NC; ++c) {
+                        uint32_t lo, hi;
+                        nl4_decode_dword(cw[c][j], lo, hi);
+                        bv[c] = (long)(((uint64_t)hi << 32) | lo);
                     }
-                    const float4 x4 = *(const float4 *)&s_xs[t][b][4 * g];
+                    // fp16 weight scales; x * dw below is one v_fma_mix_f32 (fp16 operand
+                    // widened exactly, + 0, one rounding: the same value as a multiply)
+                    typedef _Float16 hNC __attribute__((ext_vector_type(NC)));
+                    const hNC dw = *(const hNC *)(lds + LY::DW + (((8 * ch + s) * 4 + wv) * 16 + n) * NC * 2);
+                    // per tile: NC exact block dots on the matrix cores, then the fp32 scaling
 #pragma unroll
-                    for (int c = 0; c < 4; ++c) {
-                        acc[c][t][0] = fmaf((float)P[c][0], x4.x * dw[c], acc[c][t][0]);
-                        acc[c][t][1] = fmaf((float)P[c][1], x4.y * dw[c], acc[c][t][1]);
-                        acc[c][t][2] = fmaf((float)P[c][2], x4.z * dw[c], acc[c][t][2]);
-                        acc[c][t][3] = fmaf((float)P[c][3], x4.w * dw[c], acc[c][t][3]);
+                    for (int t = 0; t < NT; ++t) {
+                        const uint4 v = av2[t];
+                        const long av = jj ? (long)(((uint64_t)v.w << 32) | v.z) : (long)(((uint64_t)v.y << 32) | v.x);
+                        typedef int i32x4 __attribute__((ext_vector_type(4)));
+                        i32x4 P[NC];
+#pragma unroll
+                        for (int c = 0; c < NC; ++c) {
+                            const i32x4 zero = {0, 0, 0, 0};
+                            P[c] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bv[c], zero, 0, 0, 0);
+                        }
+                        const float4 x4 = *(const float4 *)(xsl + s * 16 * NT + 16 * t + 4 * g);
+#pragma unroll
+                        for (int c = 0; c < NC; ++c) {
+                            const float dwc = (float)dw[c];
+                            acc[c][t][0] = fmaf((float)P[c][0], fmaf(x4.x, dwc, 0.f), acc[c][t][0]);
+                            acc[c][t][1] = fmaf((float)P[c][1], fmaf(x4.y, dwc, 0.f), acc[c][t][1]);
+                            acc[c][t][2] = fmaf((float)P[c][2], fmaf(x4.z, dwc, 0.f), acc[c][t][2]);
+                            acc[c][t][3] = fmaf((float)P[c][3], fmaf(x4.w, dwc, 0.f), acc[c][t][3]);
+                        }
                     }
-                }
-                if (s & 1) {
-                    // last read of the pair slot done (every tile's accumulators
-                    // depend on it): refill the slot (see above)
-                    uint32_t dep;
-                    if (NT == 1)
-                        asm volatile("v_mov_b32 %0, 0" : "=v"(dep) : "v"(acc[0][0][0]));
-                    else if (NT == 2)
-                        asm volatile("v_mov_b32 %0, 0" : "=v"(dep) : "v"(acc[0][0][0]), "v"(acc[0][NT - 1][0]));
-                    else
-                        asm volatile("v_mov_b32 %0, 0" : "=v"(dep)
-                                     : "v"(acc[0][0][0]), "v"(acc[0][1][0]), "v"(acc[0][NT - 2][0]), "v"(acc[0][NT - 1][0]));
-                    load_a(nx, ps, dep);
-                    __builtin_amdgcn_sched_barrier(0);
+                    // scale now: left alone the compiler defers the block's scaling,
+                    // keeping every block product of the turn live
+#pragma unroll
+                    for (int c = 0; c < NC; ++c)
+#pragma unroll
+                        for (int t = 0; t < NT; ++t)
+                            asm volatile("" : "+v"(acc[c][t][0]), "+v"(acc[c][t][1]), "+v"(acc[c][t][2]), "+v"(acc[c][t][3]));
                 }
             }
+        }
+        if (ch + 1 < NCH) {
+            // the other stage was last read in turn ch - 1, before the previous barrier
+            stage_store((ch + 1) & 1);
+            __syncthreads();
         }
     }
 
     // lane holds rows 16 t + 4 g + i, column n of each group
-    if (GU) {
+    if constexpr (GU && NC == 4) {
         const int jb = yb * 4 + wv; // 32-block of h
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
@@ -297,6 +343,33 @@ __device__ __forceinline__ void expert_tile(const GemmTileArgs &a, const int4 it
                 }
             }
         }
+    } else if constexpr (GU) {
+        // h rows 16 (4 yb + wv) + n: half (wv & 1) of 32-block jb
+        const int jb = yb * 2 + (wv >> 1), half = wv & 1;
+        float h[NT][4], m[NT][4];
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                h[t][i] = silu_mul(acc[0][t][i], acc[1][t][i]);
+                m[t][i] = max16(fabsf(h[t][i]));
+                if (n == 0) sm.amax[wv][16 * t + 4 * g + i] = m[t][i];
+            }
+        __syncthreads();
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                float d;
+                const float id = quant_scale_inv(fmaxf(m[t][i], sm.amax[wv ^ 1][16 * t + 4 * g + i]), d);
+                const int p = s_pair[16 * t + 4 * g + i];
+                if (p >= 0) {
+                    int8_t *hrow = a.hq + (size_t)p * QE_FF_EXP + (jb >> 1) * 64 + (n >> 2) * 16 + (jb & 1) * 8 + (n & 3);
+                    hrow[4 * half] = quant_one(h[t][i], id);
+                    if (n == 0 && half == 0) a.hs[(size_t)p * (QE_FF_EXP / 32) + jb] = d;
+                }
+            }
+        }
     } else {
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
@@ -307,26 +380,37 @@ __device__ __forceinline__ void expert_tile(const GemmTileArgs &a, const int4 it
                 const float w = a.wts[p];
                 float *yrow = a.yp + (size_t)p * QE_D;
 #pragma unroll
-                for (int c = 0; c < 4; ++c) yrow[rowc[c]] = w * acc[c][t][i];
+                for (int c = 0; c < NC; ++c) yrow[rowc[c]] = w * acc[c][t][i];
             }
         }
     }
 }
 
-// One launch per GEMM; an item of <= 16 pairs runs the one-tile body.
-template <bool GU> QE_DEV void expert_item(const GemmTileArgs &a, int item, int yb, ExpertSmem<GU> &sm) {
-    if (item >= *a.n_items) return;
+// Every item runs NC = 2: gate/up over 8 row groups of 64 h rows, down over 16
+// of 128 output rows; workgroup b = (item b / RG, row group b % RG).  Big items
+// (33..64 pairs) run NT = 4, small ones NT = 2 or 1.
+template <bool GU> constexpr int expert_rg() { return GU ? QE_FF_EXP / 64 : QE_D / 128; }
+template <bool GU> QE_DEV void expert_unit(const GemmTileArgs &a, int b, ExpertSmem<GU> &sm) {
+    constexpr int RG = expert_rg<GU>();
+    const int item = b / RG, yb = b % RG;
+    if (item >= a.n_items[0]) return;
     const int4 it = a.items[item];
-    static_assert(QE_MFMA_MC == 32, "items of up to two 16-row tiles");
-    if (it.z > 16)
-        expert_tile<GU, 2>(a, it, yb, sm);
+    static_assert(QE_MFMA_MC == 64, "items of up to four 16-row tiles");
+    if (it.z > 32)
+        expert_tile<GU, 2, 4>(a, it, yb, sm);
+    else if (it.z > 16)
+        expert_tile<GU, 2, 2>(a, it, yb, sm);
     else
-        expert_tile<GU, 1>(a, it, yb, sm);
+        expert_tile<GU, 2, 1>(a, it, yb, sm);
 }
-// Workgroup (row group y, item) with y fastest: an item's row groups run together.
+// Upper bound of the workgroups over the items of np pairs: items of more than
+// QE_MFMA_MC / 2 pairs, plus at most one smaller item per expert.
+template <bool GU> constexpr int expert_max_wg(int np) {
+    return expert_rg<GU>() * (np / (QE_MFMA_MC / 2 + 1) + 1 + QE_N_EXPERT);
+}
 __global__ __launch_bounds__(256, 2) void k_expert_gu(GemmTileArgs a) {
     __shared__ ExpertSmem<true> sm;
-    expert_item<true>(a, blockIdx.y, blockIdx.x, sm);
+    expert_unit<true>(a, blockIdx.x, sm);
 }
 
 
@@ -608,12 +692,12 @@ QE_DEV void shdn_tile(const _Float16 *hhl, int T, const uint8_t *W, float *out, 
 // Routed down items and shared down tiles in one launch: the routed items
 // (item, then row group) come first, the shared tiles fill the CUs as the
 // routed work drains.
-__global__ __launch_bounds__(256, 2) void k_expert_dn(GemmTileArgs a, int max_items, const _Float16 *hhl, int T,
+__global__ __launch_bounds__(256, 2) void k_expert_dn(GemmTileArgs a, int nr, const _Float16 *hhl, int T,
                                                       const uint8_t *Wsd, float *sd) {
     __shared__ ExpertSmem<false> sm;
-    const int nr = max_items * (QE_D / 256), b = blockIdx.x;
+    const int b = blockIdx.x;
     if (b < nr) {
-        expert_item<false>(a, b / (QE_D / 256), b % (QE_D / 256), sm);
+        expert_unit<false>(a, b, sm);
     } else {
         const int s = b - nr, mt = (T + 31) / 32;
         shdn_tile(hhl, T, Wsd, sd, s % mt, s / mt);
@@ -628,13 +712,13 @@ hipError_t qe_launch_router_shgu(const QeLayerPtrs &L, const QeScratch &S, int T
 
 hipError_t qe_launch_expert_mfma(const QeLayerPtrs &L, const QeScratch &S, int T, hipStream_t st) {
     const int np = T * QE_K_USED;
-    const int max_items = np / QE_MFMA_MC + QE_N_EXPERT;
     GemmTileArgs g{};
     g.arena = L.arena; g.pairs = S.pairs; g.items = S.items; g.n_items = S.n_items; g.wts = S.wts;
     g.aq = S.xqp; g.a_bytes = T * QE_D; g.as = S.xs; g.a_row_div = QE_K_USED; g.hq = S.hqp; g.hs = S.hs;
-    k_expert_gu<<<dim3(QE_FF_EXP / 128, max_items), 256, 0, st>>>(g);
+    k_expert_gu<<<expert_max_wg<true>(np), 256, 0, st>>>(g);
     g.aq = S.hqp; g.a_bytes = np * QE_FF_EXP; g.as = S.hs; g.a_row_div = 1; g.yp = S.yp;
     const int nsh = ((T + 31) / 32) * (QE_D / 128);
-    k_expert_dn<<<max_items * (QE_D / 256) + nsh, 256, 0, st>>>(g, max_items, (const _Float16 *)S.shgu, T, L.sh_dn, S.sd);
+    const int nr = expert_max_wg<false>(np);
+    k_expert_dn<<<nr + nsh, 256, 0, st>>>(g, nr, (const _Float16 *)S.shgu, T, L.sh_dn, S.sd);
     return hipGetLastError();
 }
