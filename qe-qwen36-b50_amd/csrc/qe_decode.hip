@@ -181,7 +181,7 @@ QE_DEV void unit_rows(const uint8_t *row, int c, int row_in_unit, const int4 it,
 #pragma unroll
         for (int i = 0; i < NB; ++i) {
             const int b = c + LPR * i;
-            const nl4_blk w = nl4_decode_block(q[i]); // decoded per pair: few registers, T > 1 only repeats
+            const nl4_blk w = nl4_decode_block<NB == 2>(q[i]); // decoded per pair: few registers, T > 1 only repeats
             const uint4 x0 = *(const uint4 *)(xq + b * 32), x1 = *(const uint4 *)(xq + b * 32 + 16);
             acc = fmaf(dw[i] * xs[b], (float)nl4_block_dot(w, x0, x1), acc);
         }
@@ -684,7 +684,7 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
                     q = *(const uint4 *)(drow + l16 * 16);
                     sraw = ((const uint16_t *)(drow + QE_FF_EXP / 2))[l16];
                 }
-                const nl4_blk w = nl4_decode_block(q);
+                const nl4_blk w = nl4_decode_block<TM == 1>(q); // T > 1: at the register limit
                 const float sc = f16_bits_to_f32(sraw);
                 const int npair = act ? it.z : 0;
                 for (int j = 0; j < T; ++j) { // pairs of the item (<= T); wave-uniform trip count

@@ -21,31 +21,36 @@ QE_DEV uint32_t nl4_lookup4(uint32_t idx /* 4 indices, one per byte, 0..15 */) {
     const uint32_t sel = ((idx >> 1) & 0x04040404u) | 0x03020100u;     // bit 3 -> take b
     return __builtin_amdgcn_perm(b, a, sel);
 }
-// (v & 0x04040404) | 0x03020100 in one v_and_or_b32.  GFX9 VOP3 takes no
-// literal and one SGPR, so the mask rides in an SGPR and the byte ramp in a
-// VGPR (both loop-invariant); plain C gets an and plus an or.
-QE_DEV uint32_t nl4_merge_sel(uint32_t v) {
-    uint32_t r;
-    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(v), "s"(0x04040404u), "v"(0x03020100u));
-    return r;
+// (v & 0x04040404) | 0x03020100.  VOP3 = true: one v_and_or_b32 (GFX9 VOP3
+// takes no literal and one SGPR, so the mask rides in an SGPR and the byte
+// ramp in a VGPR held across the loop); plain C: an and plus an or, no VGPR
+// held (for kernels at their register limit).
+template <bool VOP3> QE_DEV uint32_t nl4_merge_sel(uint32_t v) {
+    if constexpr (VOP3) {
+        uint32_t r;
+        asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(v), "s"(0x04040404u), "v"(0x03020100u));
+        return r;
+    } else {
+        return (v & 0x04040404u) | 0x03020100u;
+    }
 }
 // Both nibbles of 4 code bytes; the bit-3 selector comes straight from the
 // code bytes (bits 3 and 7), without extracting the nibbles first.
-QE_DEV void nl4_decode_dword(uint32_t q, uint32_t &lo, uint32_t &hi) {
+template <bool VOP3 = false> QE_DEV void nl4_decode_dword(uint32_t q, uint32_t &lo, uint32_t &hi) {
     const uint32_t il = q & 0x07070707u, ih = (q >> 4) & 0x07070707u;
-    const uint32_t sl = nl4_merge_sel(q >> 1), sh = nl4_merge_sel(q >> 5);
+    const uint32_t sl = nl4_merge_sel<VOP3>(q >> 1), sh = nl4_merge_sel<VOP3>(q >> 5);
     lo = __builtin_amdgcn_perm(__builtin_amdgcn_perm(QE_NL4_W3, QE_NL4_W2, il), __builtin_amdgcn_perm(QE_NL4_W1, QE_NL4_W0, il), sl);
     hi = __builtin_amdgcn_perm(__builtin_amdgcn_perm(QE_NL4_W3, QE_NL4_W2, ih), __builtin_amdgcn_perm(QE_NL4_W1, QE_NL4_W0, ih), sh);
 }
 // Decoded 32-weight block: w[0..3] = elements 0..15, w[4..7] = elements 16..31,
 // each dword holding 4 consecutive elements.
 struct nl4_blk { uint32_t w[8]; };
-QE_DEV nl4_blk nl4_decode_block(uint4 q) {
+template <bool VOP3 = false> QE_DEV nl4_blk nl4_decode_block(uint4 q) {
     nl4_blk r;
-    nl4_decode_dword(q.x, r.w[0], r.w[4]);
-    nl4_decode_dword(q.y, r.w[1], r.w[5]);
-    nl4_decode_dword(q.z, r.w[2], r.w[6]);
-    nl4_decode_dword(q.w, r.w[3], r.w[7]);
+    nl4_decode_dword<VOP3>(q.x, r.w[0], r.w[4]);
+    nl4_decode_dword<VOP3>(q.y, r.w[1], r.w[5]);
+    nl4_decode_dword<VOP3>(q.z, r.w[2], r.w[6]);
+    nl4_decode_dword<VOP3>(q.w, r.w[3], r.w[7]);
     return r;
 }
 // Exact int32 dot of a decoded block with 32 int8 activations (two uint4).

@@ -275,7 +275,7 @@ __device__ __forceinline__ void expert_tile(const GemmTileArgs &a, const int4 it
 #pragma unroll
                     for (int c = 0; c < NC; ++c) {
                         uint32_t lo, hi;
-                        nl4_decode_dword(cw[c][j], lo, hi);
+                        nl4_decode_dword<true>(cw[c][j], lo, hi);
                         bv[c] = (long)(((uint64_t)hi << 32) | lo);
                     }
                     // fp16 weight scales; x * dw below is one v_fma_mix_f32 (fp16 operand
