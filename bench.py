@@ -9,6 +9,9 @@ HBM arena, inputs resident in HBM before timing.  Also reported:
   * prefill512_tflops: BASELINE config 3 (512 tokens, one layer, Zipf s=1
     router bias), 29.53 GFLOP per call / time, with its roofline (AI x HBM
     peak vs the fp16 MFMA peak) and the routed grouped-GEMM rate alone;
+  * prefill8192_zipf13: BASELINE config 4 (8192 tokens, one layer, Zipf s=1.3),
+    472.5 GFLOP per call / time;
+  * decode_b8: 8 tokens per step through the 40-layer stack;
   * roofline: the decode kernel (k_decode, the only kernel of a decode step)
     timed with the library's HIP events on the launch stream over a profiled
     pass of the same workload;
@@ -119,6 +122,7 @@ def main():
     ap.add_argument("--graph", action="store_true", help="replay a captured HIP graph (one launch per step anyway)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--prefill-configs", default="3,4", help="BASELINE prefill configs to run (3: 512 tokens, 4: 8192)")
     ap.add_argument("--cpu-layers", type=int, default=8, help="distinct synthetic layers cycled by the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="timed CPU work of the baseline sample")
     ap.add_argument("--cpu-threads", type=int, default=16, help="host threads of the CPU baseline (the box's CPU share)")
@@ -223,11 +227,11 @@ def main():
 
     # ---------------- config 3: prefill 512, one layer ----------------
     pre = {}
-    if not args.no_prefill:
+    pcfg = set() if args.no_prefill else {c.strip() for c in args.prefill_configs.split(",")}
+    if pcfg:
         sys.path.insert(0, os.path.join(REPO, "oracle"))
-        bias = np.empty(256, np.float32)
         import oracle as O
-
+    if "3" in pcfg:
         bias = O.gen_zipf_bias(SEED, 0, 1.0)
         mp = qe_moe.MoE(n_layers=1, t_max=512)
         mp.synth_layer(0, SEED, bias, stream=stream)
@@ -268,7 +272,30 @@ def main():
                                       "top8_share": round(float(np.sort(cnt)[-8:].sum() / cnt.sum()), 4),
                                       "experts_lt4_tokens": int(((cnt > 0) & (cnt < 4)).sum())},
                "prefill512_kernels_us": {k: round(v[0] / v[1] * 1e3, 2) for k, v in pk.items()}}
-        del mp
+        del mp, xp, yp
+        torch.cuda.empty_cache()
+
+    if "4" in pcfg:
+        # config 4: prefill 8192, one layer, Zipf s=1.3 router bias
+        T4 = 8192
+        m4 = qe_moe.MoE(n_layers=1, t_max=T4)
+        m4.synth_layer(0, SEED, O.gen_zipf_bias(SEED, 0, 1.3), stream=stream)
+        x4 = torch.empty(T4, 2048, device=dev)
+        qe_moe.synth_x(SEED, 4, x4, x4.numel(), stream=stream)
+        y4 = torch.empty_like(x4)
+        for _ in range(2):
+            m4.forward_normed(0, x4, y4, T4, stream=torch.cuda.current_stream())
+        ms4 = timed(torch, lambda: m4.forward_normed(0, x4, y4, T4, stream=torch.cuda.current_stream()),
+                    max(3, args.steps // 40), torch.cuda.current_stream())
+        c4 = np.diff(m4.routing(T4)["off"])
+        f4 = T4 * FLOP_PER_TOKEN
+        pre["prefill8192_zipf13"] = {"ms": round(ms4, 4), "tflops": round(f4 / (ms4 / 1e3) / 1e12, 2),
+                                     "frac_fp16_peak": round(f4 / (ms4 / 1e3) / FP16_PEAK, 4),
+                                     "distinct_experts": int(np.count_nonzero(c4)), "max_tokens_per_expert": int(c4.max()),
+                                     "top8_share": round(float(np.sort(c4)[-8:].sum() / c4.sum()), 4),
+                                     "experts_lt4_tokens": int(((c4 > 0) & (c4 < 4)).sum())}
+        del m4, x4, y4
+        torch.cuda.empty_cache()
 
     # ---------------- CPU baseline ----------------
     cpu = None

@@ -10,7 +10,7 @@
 // path to fp32 rounding.  (Scaled fp16/bf16 operands would not: the h
 // quantisation downstream turns 1e-4 relative noise into >1e-3 output error.)
 //
-// Work item: (expert e, up to 32 of its pairs in dispatch order) x row group.
+// Work item: (expert e, up to 64 of its pairs in dispatch order) x row group.
 //   gate/up epilogue: h = silu(g)*u, quantised per 32-block (the quant_x step
 //   of engine/qe.cpp:2078-2081), stored int8 in the operand layout + fp32 scales;
 //   down epilogue: yp[p][n] = w_p * y.
@@ -50,7 +50,7 @@ struct GemmTileArgs {
     const float *as;           // their fp32 block scales
     int a_row_div;             // pair -> activation row: p / a_row_div (8 for tokens, 1 for pairs)
     const int32_t *pairs;
-    const int4 *items;         // (expert, first pair, count <= 32)
+    const int4 *items;         // (expert, first pair, count <= QE_MFMA_MC)
     const int32_t *n_items;
     const float *wts;          // pair weights (down)
     int8_t *hq; float *hs;     // gate/up output: quantised h (operand layout) + block scales
