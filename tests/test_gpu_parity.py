@@ -162,6 +162,32 @@ def test_prefill_ragged_T(ctx, torch_cuda, T, norm):
     check_layer(L, g, x, norm=norm)
 
 
+@pytest.mark.parametrize("T", [16, 17, 32, 33, 64, 65, 130])
+def test_prefill_item_boundaries(ctx, torch_cuda, T):
+    # A large bias on 8 experts routes every token to them, so each holds exactly
+    # T pairs and the work items take every size class: 16 | 17 (one 16-pair
+    # tile | two), 32 | 33 (two tiles | four), 64 | 65 (a full item | plus a
+    # one-pair remainder), 130 (two full items and a two-pair remainder).
+    torch = torch_cuda
+    say(f"prefill item boundaries: 8 experts x {T} pairs")
+    bias = np.zeros(256, np.float32)
+    hot = [3, 40, 77, 128, 129, 200, 254, 255]
+    bias[hot] = 50.0
+    L = O.SynthLayer(SEED, 0, bias=bias)
+    ctx.synth_layer(0, SEED, bias)
+    x = O.gen_x(SEED, 400 + T, T)
+    xt = torch.from_numpy(x).cuda()
+    y = torch.empty_like(xt)
+    ctx.forward_normed(0, xt, y, T)
+    torch.cuda.synchronize()
+    g = ctx.routing(T)
+    g["logits"] = ctx.logits(T)
+    g["out"] = y.cpu().numpy()
+    o = check_layer(L, g, x)
+    cnt = np.diff(o["off"])
+    assert sorted(np.flatnonzero(cnt).tolist()) == hot and set(cnt[hot].tolist()) == {T}
+
+
 def tied_layer(kind):
     """Layer 1's synthetic weights with a router that forces equal logits."""
     L = O.SynthLayer(SEED, 1)
