@@ -468,11 +468,14 @@ QE_DEV float half_of(const qe_u32x4 s[2], int b) { // fp16 scale b of 16 packed 
 // three levels ((s0 + s1) + (s2 + s3)) + ((s4 + s5) + (s6 + s7)) -- bit-identical
 // to the unsplit order.  Row 256 (the shared-expert gate) is one canonical wave
 // dot per token in k_topk.  Tile 64 tokens x 64 rows, 256 threads, 4 x 4 outputs
-// per thread; chunks are double-buffered in LDS, the next one loaded into
-// registers while the current one is multiplied.
+// per thread; chunks are double-buffered in LDS, k-major, the next one loaded
+// into registers while the current one is multiplied.  The transposing stores
+// XOR the column with the k group ((k / 8) % 4 * 16), so the four k groups a
+// wave stores land in different banks; the reads undo it (float4 runs stay
+// aligned).
 struct RouterSmem {
-    float As[2][32][68];
-    float Bs[2][32][68];
+    float As[2][32][64];
+    float Bs[2][32][64];
 };
 QE_DEV void router_tile(const float *xn, int T, const float *W, float *part, int n_tile, int m_tile, int z,
                         RouterSmem &sm) {
@@ -496,10 +499,11 @@ QE_DEV void router_tile(const float *xn, int T, const float *W, float *part, int
     auto stage = [&](int buf) {
         const float va[8] = {pa[0].x, pa[0].y, pa[0].z, pa[0].w, pa[1].x, pa[1].y, pa[1].z, pa[1].w};
         const float vb[8] = {pb[0].x, pb[0].y, pb[0].z, pb[0].w, pb[1].x, pb[1].y, pb[1].z, pb[1].w};
+        const int col = lr ^ ((lk >> 3) << 4);
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            As[buf][lk + i][lr] = va[i];
-            Bs[buf][lk + i][lr] = vb[i];
+            As[buf][lk + i][col] = va[i];
+            Bs[buf][lk + i][col] = vb[i];
         }
     };
     fetch(0);
@@ -517,8 +521,9 @@ QE_DEV void router_tile(const float *xn, int T, const float *W, float *part, int
             for (int j = 0; j < 4; ++j) acc[i][j] = 0.f;
 #pragma unroll
         for (int kk = 0; kk < 32; ++kk) {
-            const float4 av = *(const float4 *)&As[buf][kk][ty * 4];
-            const float4 bv = *(const float4 *)&Bs[buf][kk][tx * 4];
+            const int sw = ((kk >> 3) & 3) << 4;
+            const float4 av = *(const float4 *)&As[buf][kk][(ty * 4) ^ sw];
+            const float4 bv = *(const float4 *)&Bs[buf][kk][(tx * 4) ^ sw];
             const float ar[4] = {av.x, av.y, av.z, av.w}, br[4] = {bv.x, bv.y, bv.z, bv.w};
 #pragma unroll
             for (int i = 0; i < 4; ++i)
