@@ -95,6 +95,9 @@ QE_DEV float tv_val(uint64_t w) { return __uint_as_float((unsigned)w); }
 
 // Read N tagged words w[i] = src[i * stride] until every one carries `tag`
 // (wave-uniform retry, bounded; a timeout sets *err).  Inactive lanes read nothing.
+// One read in flight per retry: measured against two, four and six staggered
+// reads per poller, the extra polling traffic delayed the producers' stores
+// more than it shortened detection (1,680 vs 1,620 / 1,551 / 1,494 tokens/s).
 template <int N>
 QE_DEV void read_tv(const uint64_t *src, int stride, unsigned tag, uint64_t w[N], bool act, unsigned *err) {
     for (int spins = 0;; ++spins) {
@@ -107,48 +110,6 @@ QE_DEV void read_tv(const uint64_t *src, int stride, unsigned tag, uint64_t w[N]
         if (__all(bad == 0)) break;
         if (spins > SPIN_CAP) { ST_A(err, 1u); break; }
         __builtin_amdgcn_s_sleep(1);
-    }
-}
-
-// As read_tv, with two reads of the N words in flight (polls of small data
-// that is usually not there yet: logits, shared activations).
-template <int N>
-QE_DEV void poll_tv2(const uint64_t *src, int stride, unsigned tag, uint64_t w[N], bool act, unsigned *err) {
-    uint64_t b[2][N];
-    auto issue = [&](uint64_t *d) {
-#pragma unroll
-        for (int i = 0; i < N; ++i) d[i] = act ? LD_A((uint64_t *)src + (size_t)i * stride) : ((uint64_t)tag << 32);
-    };
-    auto ok = [&](const uint64_t *d) {
-        unsigned bad = 0;
-#pragma unroll
-        for (int i = 0; i < N; ++i) bad |= (unsigned)(d[i] >> 32) ^ tag;
-        return __all(bad == 0);
-    };
-    issue(b[0]);
-    __builtin_amdgcn_s_sleep(4);
-    issue(b[1]);
-    for (int spins = 0;; spins += 2) {
-        if (ok(b[0])) {
-#pragma unroll
-            for (int i = 0; i < N; ++i) w[i] = b[0][i];
-            return;
-        }
-        issue(b[0]);
-        __builtin_amdgcn_s_sleep(4);
-        if (ok(b[1])) {
-#pragma unroll
-            for (int i = 0; i < N; ++i) w[i] = b[1][i];
-            return;
-        }
-        issue(b[1]);
-        __builtin_amdgcn_s_sleep(4);
-        if (spins > SPIN_CAP) {
-            ST_A(err, 1u);
-#pragma unroll
-            for (int i = 0; i < N; ++i) w[i] = b[1][i];
-            return;
-        }
     }
 }
 
@@ -290,7 +251,7 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
         }
         if (li > 0 && tid < T * 256) { // x: one word per (8-row group, token) polled first; the
             uint64_t w[1];               // rest of the workgroup polls its own words directly
-            poll_tv2<1>(src_x + (tid >> 8) * QE_D + (tid & 255) * 8 + 7, 0, tagIn, w, true, a.err);
+            read_tv<1>(src_x + (tid >> 8) * QE_D + (tid & 255) * 8 + 7, 0, tagIn, w, true, a.err);
         }
         // raw x of all tokens -> LDS (natural layout, token stride 2048; T*2048 is a multiple of 2 NTH)
         if (li == 0) {
@@ -423,8 +384,8 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
         if (wv < T) {
             const int t = wv;
             uint64_t w[5];
-            poll_tv2<4>(EXr + EX_L + t * QE_ROUTER_ROWS + lane, 64, tagR, w, true, a.err);
-            poll_tv2<1>(EXr + EX_L + t * QE_ROUTER_ROWS + QE_N_EXPERT, 0, tagR, w + 4, true, a.err);
+            read_tv<4>(EXr + EX_L + t * QE_ROUTER_ROWS + lane, 64, tagR, w, true, a.err);
+            read_tv<1>(EXr + EX_L + t * QE_ROUTER_ROWS + QE_N_EXPERT, 0, tagR, w + 4, true, a.err);
             float v[5];
 #pragma unroll
             for (int j = 0; j < 5; ++j) v[j] = tv_val(w[j]);
@@ -630,7 +591,7 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
         }
         if (mode16 && tid < 256) {
             uint64_t w[1];
-            poll_tv2<1>(EXr + EX_HF + (tid >> 5) * QE_FF_EXP + (tid & 31) * 16 + 15, 0, tagG, w, true, a.err);
+            read_tv<1>(EXr + EX_HF + (tid >> 5) * QE_FF_EXP + (tid & 31) * 16 + 15, 0, tagG, w, true, a.err);
         }
         if (mode16) { // fp32 h of the 8 pairs -> LDS, then int8 per 32 rows
             // thread = 4 consecutive h of one pair, 8 lanes per 32-block (quant_x per block)
