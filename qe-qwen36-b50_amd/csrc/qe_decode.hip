@@ -22,7 +22,7 @@
 // of x and h, one word per producer first (the last it writes), then all of it
 // once with the tags verified (a word not there yet is re-read).
 // Every exchanged buffer exists in REP copies: producers write all of them, a
-// workgroup reads copy blockIdx % REP, so ~32 workgroups poll any one cache
+// workgroup reads copy blockIdx % REP, so ~64 workgroups poll any one cache
 // line instead of all 256 (the shared lines otherwise queue the polls at
 // their memory channel: ~5 us per exchange against a 0.6 us one-way
 // store->load latency measured between two workgroups).

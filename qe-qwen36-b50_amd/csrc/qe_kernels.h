@@ -88,7 +88,7 @@ struct QeDecodeArgs {
 };
 hipError_t qe_launch_decode(const QeDecodeArgs &a, hipStream_t st);
 #ifndef QE_DEC_REP
-#define QE_DEC_REP 8 /* copies of every decode exchange buffer and stage counter */
+#define QE_DEC_REP 4 /* copies of every decode exchange buffer */
 #endif
 #define QE_DECODE_EX_WORDS \
     (QE_DEC_REP * (2 * QE_SMALL_T * QE_D + QE_SMALL_T * QE_ROUTER_ROWS + QE_SMALL_T * QE_FF_SH + QE_SMALL_T * 8 * 16 * 9 + 8 * QE_FF_EXP))
