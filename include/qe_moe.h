@@ -76,6 +76,16 @@ int qe_moe_set_dense(qe_moe_ctx *ctx, int layer, const float *post_norm, const f
  * decode (:2466-2572) / decode_multi (:1653-1737).  x may not alias x2. */
 int qe_moe_forward(qe_moe_ctx *ctx, int layer, const float *x2, float *x, int T, void *stream);
 
+/* As qe_moe_forward, then the next block's input norm on the result:
+ * xn = RMSNorm(x) * next_norm (fp32 [2048], device memory), in the same
+ * canonical order as the entry norm.  Replaces Engine::moe_batched
+ * (engine/qe.cpp:1957) followed by the next layer's
+ * rmsnorm_rows(X, attn_norm, XN) (:1280), or by the final out_norm (:1295);
+ * in decode, the MoE block (:2466-2572) followed by rmsnorm(x, attn_norm, xn)
+ * (:2243) or out_norm (:2574).  xn may not alias x or x2. */
+int qe_moe_forward_norm(qe_moe_ctx *ctx, int layer, const float *x2, float *x, int T, const float *next_norm, float *xn,
+                        void *stream);
+
 /* MoE on already-normalised input, no residual: y = MoE(xn).  The "one MoE
  * layer" of the benchmark configurations; the same kernels as qe_moe_forward
  * with the norm and the residual switched off. */

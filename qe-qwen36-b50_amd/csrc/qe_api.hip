@@ -318,7 +318,7 @@ static int check_fwd(qe_moe_ctx *c, int layer, const void *in, const void *out, 
 
 // T <= QE_SMALL_T: every layer of the range in one persistent launch.
 static hipError_t run_decode(qe_moe_ctx *c, int first, int n, const float *in, float *out, int T, bool norm_res,
-                             hipStream_t st) {
+                             hipStream_t st, const float *exit_norm = nullptr, float *exit_xn = nullptr) {
     QeDecodeArgs d{};
     d.arena = c->arena; d.router = c->router; d.bias = c->bias; d.bias_on = c->bias_on;
     d.sh_gu = c->sh_gu; d.sh_dn = c->sh_dn; d.post_norm = c->post_norm;
@@ -328,6 +328,7 @@ static hipError_t run_decode(qe_moe_ctx *c, int first, int n, const float *in, f
     d.logits = c->S.logits; d.ids = c->S.ids; d.wts = c->S.wts; d.shg = c->S.shg; d.off = c->S.off; d.pairs = c->S.pairs;
     d.sd_out = c->S.sd; d.xn_out = c->S.xn;
     d.sync = c->sync; d.err = c->err;
+    d.exit_norm = exit_norm; d.exit_xn = exit_xn;
     ProfScope ps(&c->prof, QP_DECODE, st);
     return qe_launch_decode(d, st);
 }
@@ -338,6 +339,20 @@ int qe_moe_forward(qe_moe_ctx *c, int layer, const float *x2, float *x, int T, v
     HIP_TRY(hipSetDevice(c->device));
     if (T <= QE_SMALL_T) HIP_TRY(run_decode(c, layer, 1, x2, x, T, true, (hipStream_t)stream));
     else HIP_TRY(qe_launch_layer(layer_ptrs(c, layer), c->S, x2, true, x2, x, T, (hipStream_t)stream));
+    return QE_OK;
+}
+
+int qe_moe_forward_norm(qe_moe_ctx *c, int layer, const float *x2, float *x, int T, const float *next_norm, float *xn,
+                        void *stream) {
+    int rc = check_fwd(c, layer, x2, x, T);
+    if (rc) return rc;
+    if (!next_norm || !xn) return fail(QE_ERR_ARG, "forward_norm: next_norm and xn are required");
+    if (xn == x || xn == x2) return fail(QE_ERR_ARG, "forward_norm: xn may not alias x or x2");
+    HIP_TRY(hipSetDevice(c->device));
+    if (T <= QE_SMALL_T)
+        HIP_TRY(run_decode(c, layer, 1, x2, x, T, true, (hipStream_t)stream, next_norm, xn));
+    else
+        HIP_TRY(qe_launch_layer(layer_ptrs(c, layer), c->S, x2, true, x2, x, T, (hipStream_t)stream, next_norm, xn));
     return QE_OK;
 }
 

@@ -679,7 +679,8 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
                 if (last) {
                     a.x_out[o] = out;
                     if (a.sd_out) a.sd_out[o] = sd;
-                } else {
+                }
+                if (!last || a.exit_xn) { // the exit norm reads the last x like a next layer would
 #pragma unroll
                     for (int r = 0; r < REP; ++r) ST_A(dst_x + r * EX_TOTAL + o, pack_tv(out, tagD));
                 }
@@ -687,6 +688,35 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
             __syncthreads(); // s_y is rewritten by the next row group
         }
         __syncthreads(); // the LDS union is rewritten by the next layer's R stage
+    }
+
+    // Exit norm (the next block's input norm, engine/qe.cpp:2243 / :2574):
+    // workgroup t < T gathers token t of the last layer's x from the exchange
+    // and writes RMSNorm(x) * exit_norm in the canonical order.
+    if (a.exit_xn && (int)blockIdx.x < T) {
+        const int t = blockIdx.x, li = a.n_layers - 1;
+        const unsigned tagX = epoch * 65536u + (unsigned)li * 4u + 3u; // the last layer's tagD
+        const uint64_t *src = EXr + EX_X + (size_t)(li & 1) * DEC_T * QE_D + (size_t)t * QE_D;
+        for (int i = threadIdx.x; i < QE_D; i += NTH) {
+            uint64_t w[1];
+            read_tv<1>(src + i, 0, tagX, w, true, a.err);
+            s_xn[xpos(i)] = tv_val(w[0]);
+        }
+        __syncthreads();
+        if (threadIdx.x < 64) {
+            const int lane = threadIdx.x;
+            float ss = 0.f;
+#pragma unroll
+            for (int i = 0; i < 32; ++i) {
+                const float x = s_xn[i * 65 + lane];
+                ss = fmaf(x, x, ss);
+            }
+            ss = wave_sum_canon(ss);
+            if (lane == 0) s_inv[0] = 1.0f / sqrtf(ss / (float)QE_D + QE_RMS_EPS);
+        }
+        __syncthreads();
+        for (int e = threadIdx.x; e < QE_D; e += NTH)
+            a.exit_xn[(size_t)t * QE_D + e] = (s_xn[xpos(e)] * s_inv[0]) * a.exit_norm[e];
     }
 
     // the last workgroup out advances the epoch, so the next launch uses new tags

@@ -71,6 +71,7 @@ struct QeCombineArgs {
     int T;
     const float *yp; const float *sd; const float *shg; const float *x2;
     float *out;
+    const float *nw; float *xn; // optional exit norm: xn = RMSNorm(out) * nw (nw == nullptr: none)
 };
 
 // Persistent decode kernel (qe_decode.hip): T <= QE_SMALL_T tokens through
@@ -85,6 +86,7 @@ struct QeDecodeArgs {
     float *logits; int32_t *ids; float *wts; float *shg; int32_t *off; int32_t *pairs; float *sd_out; float *xn_out;
     unsigned *sync;      // QE_DECODE_SYNC_WORDS: [0] launch epoch, [32] exit counter
     unsigned *err;       // set to 1 if a poll timed out
+    const float *exit_norm; float *exit_xn; // optional: exit_xn = RMSNorm(x_out) * exit_norm
 };
 hipError_t qe_launch_decode(const QeDecodeArgs &a, hipStream_t st);
 #ifndef QE_DEC_REP
@@ -97,7 +99,8 @@ hipError_t qe_launch_decode(const QeDecodeArgs &a, hipStream_t st);
 // Launchers (qe_kernels.hip).  xin: layer input; post_norm: nullptr = input is
 // already normalised; x2: residual added to the output or nullptr.
 hipError_t qe_launch_layer(const QeLayerPtrs &L, const QeScratch &S, const float *xin, bool norm, const float *x2,
-                           float *out, int T, hipStream_t st);
+                           float *out, int T, hipStream_t st, const float *exit_norm = nullptr,
+                           float *exit_xn = nullptr);
 hipError_t qe_launch_dispatch(const QeScratch &S, int T, hipStream_t st);
 hipError_t qe_launch_expert_mfma(const QeLayerPtrs &L, const QeScratch &S, int T, hipStream_t st);
 hipError_t qe_launch_router_shgu(const QeLayerPtrs &L, const QeScratch &S, int T, hipStream_t st);

@@ -196,6 +196,62 @@ __global__ __launch_bounds__(256) void k_combine(QeCombineArgs a) {
     a.out[i] = acc;
 }
 
+// The same combine, then the next block's input norm on the result:
+// xn[t] = RMSNorm(out[t]) * nw in the canonical order of the entry norm
+// (engine/qe.cpp:1280, rmsnorm_rows of the next layer's attn_norm, or :1295
+// out_norm after the last).  Workgroup per token: every thread combines 8
+// elements (coalesced as in k_combine) into LDS, 32-element chunks padded to 33
+// words; wave 0 forms the sum of squares (lane c = chunk c, an fma chain, then
+// the pairwise tree), and every thread scales its 8 elements.
+__global__ __launch_bounds__(256) void k_combine_norm(QeCombineArgs a) {
+    __shared__ float s_x[64 * 33];
+    __shared__ float s_inv;
+    const int t = blockIdx.x, tid = threadIdx.x, e0 = tid * 8;
+    const size_t o = (size_t)t * QE_D + e0;
+    const float g = a.shg[t];
+    float v[8];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const float4 s4 = *(const float4 *)(a.sd + o + 4 * h);
+        const float4 x4 = a.x2 ? *(const float4 *)(a.x2 + o + 4 * h) : make_float4(0.f, 0.f, 0.f, 0.f);
+        v[4 * h + 0] = x4.x + g * s4.x;
+        v[4 * h + 1] = x4.y + g * s4.y;
+        v[4 * h + 2] = x4.z + g * s4.z;
+        v[4 * h + 3] = x4.w + g * s4.w;
+    }
+#pragma unroll
+    for (int k = 0; k < QE_K_USED; ++k) {
+        const float *y = a.yp + ((size_t)t * QE_K_USED + k) * QE_D + e0;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const float4 y4 = *(const float4 *)(y + 4 * h);
+            v[4 * h + 0] += y4.x;
+            v[4 * h + 1] += y4.y;
+            v[4 * h + 2] += y4.z;
+            v[4 * h + 3] += y4.w;
+        }
+    }
+    float4 *out = (float4 *)(a.out + o);
+    out[0] = make_float4(v[0], v[1], v[2], v[3]);
+    out[1] = make_float4(v[4], v[5], v[6], v[7]);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) s_x[(e0 >> 5) * 33 + (e0 & 31) + i] = v[i];
+    __syncthreads();
+    if (tid < 64) {
+        float ss = 0.f;
+#pragma unroll
+        for (int i = 0; i < 32; ++i) ss = fmaf(s_x[tid * 33 + i], s_x[tid * 33 + i], ss);
+        ss = wave_sum_canon(ss);
+        if (tid == 0) s_inv = 1.0f / sqrtf(ss / (float)QE_D + QE_RMS_EPS);
+    }
+    __syncthreads();
+    const float inv = s_inv;
+    const float4 w0 = *(const float4 *)(a.nw + e0), w1 = *(const float4 *)(a.nw + e0 + 4);
+    float4 *xo = (float4 *)(a.xn + o);
+    xo[0] = make_float4((v[0] * inv) * w0.x, (v[1] * inv) * w0.y, (v[2] * inv) * w0.z, (v[3] * inv) * w0.w);
+    xo[1] = make_float4((v[4] * inv) * w1.x, (v[5] * inv) * w1.y, (v[6] * inv) * w1.z, (v[7] * inv) * w1.w);
+}
+
 // ===========================================================================
 // synthetic fills (one 8-byte word per thread, grid-stride)
 // ===========================================================================
@@ -229,9 +285,9 @@ __global__ void k_fill_f32(float *p, float v, int64_t n) {
 #define QE_PROF(kid) ProfScope prof_scope_##kid(S.prof, kid, st)
 
 hipError_t qe_launch_layer(const QeLayerPtrs &L, const QeScratch &S, const float *xin, bool norm, const float *x2,
-                           float *out, int T, hipStream_t st) {
+                           float *out, int T, hipStream_t st, const float *exit_norm, float *exit_xn) {
     const float *pn = norm ? L.post_norm : nullptr;
-    QeCombineArgs da{T, S.yp, S.sd, S.shg, x2, out};
+    QeCombineArgs da{T, S.yp, S.sd, S.shg, x2, out, exit_norm, exit_xn};
     {
         QE_PROF(QP_NORMQ);
         k_normq<<<(T + 3) / 4, 256, 0, st>>>(xin, T, pn, S.xn, S.xqp, S.xs, S.xhl, S.chunk_hist,
@@ -258,7 +314,10 @@ hipError_t qe_launch_layer(const QeLayerPtrs &L, const QeScratch &S, const float
     }
     {
         QE_PROF(QP_COMBINE);
-        k_combine<<<(unsigned)(((size_t)T * QE_D + 255) / 256), 256, 0, st>>>(da);
+        if (exit_norm)
+            k_combine_norm<<<T, 256, 0, st>>>(da);
+        else
+            k_combine<<<(unsigned)(((size_t)T * QE_D + 255) / 256), 256, 0, st>>>(da);
     }
     return hipGetLastError();
 }

@@ -71,6 +71,7 @@ def load(path: str = LIB_PATH):
         "qe_moe_set_dense": (i32, [vp, i32, vp, vp, vp, vp, vp, i32, vp]),
         "qe_moe_forward": (i32, [vp, i32, vp, vp, i32, vp]),
         "qe_moe_forward_normed": (i32, [vp, i32, vp, vp, i32, vp]),
+        "qe_moe_forward_norm": (i32, [vp, i32, vp, vp, i32, vp, vp, vp]),
         "qe_moe_forward_stack": (i32, [vp, i32, i32, vp, vp, i32, vp]),
         "qe_moe_get_routing": (i32, [vp, i32, vp, vp, vp, vp, vp, vp, vp]),
         "qe_moe_get_logits": (i32, [vp, i32, vp, vp]),
@@ -163,6 +164,11 @@ class MoE:
     # -- compute --
     def forward(self, layer, x2, out, T, stream=None):
         _check(_lib.qe_moe_forward(self.h, layer, _ptr(x2), _ptr(out), T, _stream(stream)))
+
+    def forward_norm(self, layer, x2, out, T, next_norm, xn, stream=None):
+        """out = x2 + MoE(RMSNorm(x2)); xn = RMSNorm(out) * next_norm (the next block's input)."""
+        _check(_lib.qe_moe_forward_norm(self.h, layer, _ptr(x2), _ptr(out), T, _ptr(next_norm), _ptr(xn),
+                                        _stream(stream)))
 
     def forward_normed(self, layer, xn, out, T, stream=None):
         _check(_lib.qe_moe_forward_normed(self.h, layer, _ptr(xn), _ptr(out), T, _stream(stream)))

@@ -22,6 +22,7 @@ def test_expert_bytes_and_argument_errors():
     assert b"bad argument" in lib.qe_moe_last_error()
     assert lib.qe_moe_create(0, 1, 0, ctypes.byref(h)) == qe_moe.QE_ERR_ARG
     assert lib.qe_moe_forward(None, 0, None, None, 1, None) == qe_moe.QE_ERR_ARG
+    assert lib.qe_moe_forward_norm(None, 0, None, None, 1, None, None, None) == qe_moe.QE_ERR_ARG
     assert lib.qe_moe_load_pack(None, b"x.pack", 0, 0, 1, None) == qe_moe.QE_ERR_ARG
     assert lib.qe_moe_destroy(None) == 0
 

@@ -126,6 +126,38 @@ def test_forward_with_norm_and_residual(ctx, torch_cuda, T):
     check_layer(L, g, x, norm=True)
 
 
+@pytest.mark.parametrize("T", [1, 5, 9, 100])
+def test_forward_with_exit_norm(ctx, torch_cuda, T):
+    # qe_moe_forward_norm: the layer output as qe_moe_forward, plus the next
+    # block's input norm of it; the norm is the canonical one, so it matches the
+    # oracle's RMSNorm of the GPU's own output bit for bit.
+    torch = torch_cuda
+    say(f"forward + exit norm T={T}")
+    x = O.gen_x(SEED, 500 + T, T)
+    L = host_layer(1, 1.0)
+    ctx.synth_layer(1, SEED, L.bias)
+    w = (1.0 + 0.25 * O.gen_x(SEED, 600, 1)[0]).astype(np.float32)  # a non-trivial norm weight
+    xt = torch.from_numpy(x).cuda()
+    wt = torch.from_numpy(w).cuda()
+    y = torch.empty_like(xt)
+    xn = torch.full_like(xt, float("nan"))
+    ctx.forward_norm(1, xt, y, T, wt, xn)
+    torch.cuda.synchronize()
+    g = ctx.routing(T)
+    g["logits"] = ctx.logits(T)
+    g["out"] = y.cpu().numpy()
+    check_layer(L, g, x, norm=True)
+    ref = O.rmsnorm(g["out"], w)
+    assert np.array_equal(xn.cpu().numpy().view(np.uint32), ref.view(np.uint32))
+    # the plain forward gives the same layer output
+    y2 = torch.empty_like(xt)
+    ctx.forward(1, xt, y2, T)
+    torch.cuda.synchronize()
+    assert torch.equal(y, y2)
+    with pytest.raises(qe_moe.QeError):
+        ctx.forward_norm(1, xt, y, T, wt, y)
+
+
 def test_cfg3_prefill_512(ctx, torch_cuda):
     say("config 3: prefill 512, Zipf s=1.0")
     x = O.gen_x(SEED, 3, 512)
