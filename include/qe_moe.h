@@ -140,6 +140,32 @@ const char *qe_moe_profile_name(int id);
  * Synchronous: returns once the copies are done. */
 int qe_moe_load_pack(qe_moe_ctx *ctx, const char *path, int pack_first, int first_layer, int n_layers, void *stream);
 
+/* IQ4_NL conversion (the converter, engine/qconv.cpp).  Source tensors are
+ * ggml tensors in device memory, contiguous 32-element blocks of one of these
+ * ggml type ids (ggml.h enum ggml_type): F32 (128 B), F16 and BF16 (64 B),
+ * Q8_0 (34 B: fp16 scale d, then 32 int8; value = d * q).  Every block is
+ * quantized by ggml's IQ4_NL quantizer as the reference calls it
+ * (ggml_quantize_chunk(GGML_TYPE_IQ4_NL, ..., imatrix = NULL)), to an fp16
+ * scale and 16 code bytes in the NL4 row layout. */
+#define QE_SRC_F32 0
+#define QE_SRC_F16 1
+#define QE_SRC_Q8_0 8
+#define QE_SRC_BF16 30
+
+/* `rows` rows of `cols` source weights -> NL4 rows of cols/2 code bytes then
+ * cols/32 fp16 scales, contiguous in `dst`.  cols must be a multiple of 256,
+ * src and dst 16-byte aligned, rows * cols / 32 < 2^31.  Replaces quant_row
+ * (F_NL4) over dequant_rows' output (engine/qconv.cpp:91-98, :17-43). */
+int qe_moe_nl4_quantize_rows(const void *src, int src_type, int64_t rows, int cols, void *dst, void *stream);
+
+/* Convert one layer's routed experts into the arena of `layer`: gate and up
+ * are blk.N.ffn_gate_exps / ffn_up_exps ([256][512][2048] weights), down is
+ * blk.N.ffn_down_exps ([256][2048][512]), all of src_type.  Expert e's blob
+ * gets its 512 gate rows, 512 up rows and 2048 down rows, which is the pack's
+ * blk.N.experts entry.  Replaces convert_experts (engine/qconv.cpp:202-227). */
+int qe_moe_convert_experts(qe_moe_ctx *ctx, int layer, const void *gate, const void *up, const void *down,
+                           int src_type, void *stream);
+
 /* Device pointer of a layer's expert arena (256 blobs), for callers that fill
  * it in place. */
 int qe_moe_arena_ptr(qe_moe_ctx *ctx, int layer, void **dev);

@@ -64,6 +64,10 @@ def load():
         "orc_routed": (None, [vp, i32, vp, vp, vp, vp, vp, i32]),
         "orc_combine": (None, [vp, vp, vp, vp, i32, vp]),
         "orc_baseline_layer": (f64, [vp, vp, vp, vp, vp, vp, vp, i32, i32, vp]),
+        "orc_nl4_nearest": (i32, [f32]),
+        "orc_nl4_block": (f32, [vp, vp, vp]),
+        "orc_nl4_quantize_rows": (i32, [vp, i32, i64, i32, vp]),
+        "orc_convert_expert": (i32, [vp, vp, vp, i32, i32, vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -234,3 +238,56 @@ def baseline_layer(x2, post_norm, L: SynthLayer, experts_ptrs, T, threads):
     sec = load().orc_baseline_layer(_p(x2), _p(post_norm), _p(L.router), _p(L.bias), _p(L.sh_gu), _p(L.sh_dn),
                                     ctypes.cast(experts_ptrs, ctypes.c_void_p), T, threads, _p(out))
     return sec, out
+
+
+# ---------------------------------------------------------------------------
+# IQ4_NL converter (qe_oracle.cpp: ggml's quantizer as the reference converter
+# calls it, engine/qconv.cpp:17-43, :91-98, :202-227)
+# ---------------------------------------------------------------------------
+SRC_F32, SRC_F16, SRC_Q8_0, SRC_BF16 = 0, 1, 8, 30
+SRC_BLOCK_BYTES = {SRC_F32: 128, SRC_F16: 64, SRC_Q8_0: 34, SRC_BF16: 64}
+
+
+def nl4_row_bytes(cols):
+    return cols // 2 + cols // 32 * 2
+
+
+def nl4_nearest(a):
+    return load().orc_nl4_nearest(float(a))
+
+
+def nl4_block(x):
+    """One 32-element block -> (fp16 scale bits, 16 code bytes, fp32 scale)."""
+    x = np.ascontiguousarray(x, np.float32)
+    assert x.shape == (32,)
+    d16 = np.zeros(1, np.uint16)
+    codes = np.zeros(16, np.uint8)
+    d = load().orc_nl4_block(_p(x), _p(d16), _p(codes))
+    return int(d16[0]), codes, float(d)
+
+
+def nl4_quantize_rows(src, src_type, rows, cols):
+    """src: the ggml tensor's bytes (any dtype view, contiguous blocks)."""
+    src = np.ascontiguousarray(src)
+    assert src.nbytes == rows * cols // 32 * SRC_BLOCK_BYTES[src_type]
+    out = np.empty((rows, nl4_row_bytes(cols)), np.uint8)
+    assert load().orc_nl4_quantize_rows(_p(src), src_type, rows, cols, _p(out)) == 0
+    return out
+
+
+def convert_expert(gate, up, down, src_type, e):
+    out = np.empty(EXPERT_BYTES, np.uint8)
+    gate, up, down = (np.ascontiguousarray(a) for a in (gate, up, down))
+    assert load().orc_convert_expert(_p(gate), _p(up), _p(down), src_type, e, _p(out)) == 0
+    return out
+
+
+def nl4_dequant_rows(rows_u8, cols):
+    """NL4 rows -> fp32 (codebook value * fp16 scale), for error statistics."""
+    nb = cols // 32
+    r = np.ascontiguousarray(rows_u8).reshape(-1, nl4_row_bytes(cols))
+    codes = r[:, : cols // 2].reshape(-1, nb, 16)
+    sc = r[:, cols // 2:].copy().view(np.float16).astype(np.float32)
+    idx = np.concatenate([codes & 15, codes >> 4], axis=2)
+    kv = np.array([-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113], np.float32)
+    return (kv[idx] * sc[:, :, None]).reshape(-1, cols)

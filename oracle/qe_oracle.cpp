@@ -442,3 +442,139 @@ ORC_API double orc_baseline_layer(const float *x2, const float *post_norm, const
     orc_combine(post_norm ? x2 : nullptr, shg.data(), sd.data(), yp.data(), T, out);
     return std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
 }
+
+// ---------------------------------------------------------------------------
+// IQ4_NL conversion of routed-expert weights (the converter, off the inference
+// path).  Follows the reference converter:
+//   source block -> fp32 ..... engine/qconv.cpp:17-43 (dequant_rows: F32 as is,
+//                              F16 widened, Q8_0 as fp32(d) * q; BF16 through
+//                              ggml's to_float, which is the exact widening)
+//   NL4 row .................. engine/qconv.cpp:91-98 (ggml's block_iq4_nl, an
+//                              fp16 scale + 16 code bytes, split into the row's
+//                              code area and its scale area, :48)
+//   expert blob .............. engine/qconv.cpp:202-227 (expert e: its 512 gate
+//                              rows, 512 up rows, 2048 down rows)
+// The quantizer itself is ggml's, a dependency the reference links from a
+// llama.cpp checkout (README.md:42, engine/build.sh:4) whose version it does
+// not record: ggml_quantize_chunk(GGML_TYPE_IQ4_NL, ..., imatrix = NULL) runs
+// ggml-quants.c's quantize_iq4_nl, i.e. quantize_row_iq4_nl_impl with one
+// 32-element block per super-block, no importance weights and ntry = 7, and
+// best_index_int8 for the nearest codebook entry.  Restated from that
+// published algorithm:
+//   * m = the first element of largest |x|; a block with |m| < 1e-15 gets
+//     scale 0 (and every code the nearest entry to 0, index 8);
+//   * weights w_j = x_j^2; a candidate inverse scale s assigns
+//     q_j = nearest(s * x_j) and yields S_xq = sum w q x, S_qq = sum w q q,
+//     summed in element order with (w*q)*x and (w*q)*q;
+//   * the first candidate is s = 1 / (m / 127) and its fit d = S_xq / S_qq,
+//     best = d * S_xq; then s = (t - 127) / m for t = -7..7 replaces them when
+//     S_qq > 0 and S_xq^2 > best * S_qq;
+//   * the fp32 scale d is stored as fp16 (round to nearest even), and the codes
+//     are nearest((1/d) * x_j) with the fp32 d (0 for d = 0);
+//   * code byte j = code_j | code_{j+16} << 4.
+// ggml's quantizer sits in libggml-base, compiled without -march flags, so its
+// fp32 arithmetic is plain SSE: no contraction, which -ffp-contract=off keeps.
+// Parity with ggml's own output is unpinned (no ggml build or output vectors
+// exist here); tests/test_oracle_pins.py pins the nearest-entry rule by brute
+// force, the search by exact-fit blocks and by the optimality of the chosen
+// candidate, and the byte layout through the NL4 dot above.
+// ---------------------------------------------------------------------------
+enum { ORC_SRC_F32 = 0, ORC_SRC_F16 = 1, ORC_SRC_Q8_0 = 8, ORC_SRC_BF16 = 30 }; /* ggml type ids */
+
+static int src_block_bytes(int type) {
+    return type == ORC_SRC_F32 ? 128 : type == ORC_SRC_F16 || type == ORC_SRC_BF16 ? 64 : type == ORC_SRC_Q8_0 ? 34 : 0;
+}
+
+static void src_block(const uint8_t *src, int type, int64_t blk, float *x) {
+    const uint8_t *p = src + blk * src_block_bytes(type);
+    for (int i = 0; i < 32; ++i) {
+        uint16_t h;
+        uint32_t u;
+        switch (type) {
+        case ORC_SRC_F32: memcpy(&x[i], p + 4 * i, 4); break;
+        case ORC_SRC_F16: memcpy(&h, p + 2 * i, 2); x[i] = qe_f16_to_f32(h); break;
+        case ORC_SRC_BF16: memcpy(&h, p + 2 * i, 2); u = (uint32_t)h << 16; memcpy(&x[i], &u, 4); break;
+        default: memcpy(&h, p, 2); x[i] = qe_f16_to_f32(h) * (float)(int8_t)p[2 + i]; break;
+        }
+    }
+}
+
+ORC_API int orc_nl4_nearest(float a) {
+    const int8_t *v = QE_KVALUES_NL4;
+    if (a <= v[0]) return 0;
+    if (a >= v[15]) return 15;
+    int lo = 0, hi = 15; // v[lo] <= a < v[hi]
+    while (hi - lo > 1) {
+        const int mid = (lo + hi) / 2;
+        if (a < v[mid]) hi = mid;
+        else lo = mid;
+    }
+    return a - v[lo] < v[hi] - a ? lo : hi;
+}
+
+static void nl4_fit(const float *x, float s, float *sxq, float *sqq) {
+    float a = 0.f, b = 0.f;
+    for (int j = 0; j < 32; ++j) {
+        const float q = QE_KVALUES_NL4[orc_nl4_nearest(s * x[j])];
+        const float wq = (x[j] * x[j]) * q;
+        a = a + wq * x[j];
+        b = b + wq * q;
+    }
+    *sxq = a;
+    *sqq = b;
+}
+
+/* One 32-element block: fp16 scale and 16 code bytes; returns the fp32 scale. */
+ORC_API float orc_nl4_block(const float *x, uint16_t *d16, uint8_t *codes) {
+    float amax = 0.f, m = 0.f;
+    for (int j = 0; j < 32; ++j)
+        if (fabsf(x[j]) > amax) { amax = fabsf(x[j]); m = x[j]; }
+    float d = 0.f;
+    if (amax >= 1e-15f) {
+        float sxq, sqq;
+        nl4_fit(x, 1.f / (m / 127.f), &sxq, &sqq);
+        d = sxq / sqq;
+        float best = d * sxq;
+        for (int t = -7; t <= 7; ++t) {
+            nl4_fit(x, (float)(t - 127) / m, &sxq, &sqq);
+            if (sqq > 0.f && sxq * sxq > best * sqq) { d = sxq / sqq; best = d * sxq; }
+        }
+    }
+    *d16 = qe_f32_to_f16(d);
+    const float s = d != 0.f ? 1.f / d : 0.f;
+    int c[32];
+    for (int j = 0; j < 32; ++j) c[j] = orc_nl4_nearest(s * x[j]);
+    for (int j = 0; j < 16; ++j) codes[j] = (uint8_t)(c[j] | c[j + 16] << 4);
+    return d;
+}
+
+/* rows x cols source elements (a ggml tensor of `type`, contiguous blocks) ->
+ * NL4 rows of QE_NL4_ROW_BYTES(cols) bytes. */
+ORC_API int orc_nl4_quantize_rows(const void *src, int type, int64_t rows, int cols, uint8_t *dst) {
+    if (!src_block_bytes(type) || cols <= 0 || cols % 32) return -1;
+    const int nb = cols / 32;
+    const size_t rb = QE_NL4_ROW_BYTES(cols);
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < rows; ++r) {
+        uint8_t *row = dst + r * rb;
+        for (int b = 0; b < nb; ++b) {
+            float x[32];
+            uint16_t d16;
+            src_block((const uint8_t *)src, type, r * nb + b, x);
+            orc_nl4_block(x, &d16, row + b * 16);
+            memcpy(row + cols / 2 + 2 * b, &d16, 2);
+        }
+    }
+    return 0;
+}
+
+/* Expert e's blob from the layer's ffn_{gate,up,down}_exps tensors. */
+ORC_API int orc_convert_expert(const void *gate, const void *up, const void *down, int type, int e, uint8_t *blob) {
+    const size_t bb = (size_t)src_block_bytes(type);
+    if (!bb || e < 0 || e >= NE) return -1;
+    const size_t gu_src = (size_t)e * FF * (D / 32) * bb, dn_src = (size_t)e * D * (FF / 32) * bb;
+    orc_nl4_quantize_rows((const uint8_t *)gate + gu_src, type, FF, D, blob);
+    orc_nl4_quantize_rows((const uint8_t *)up + gu_src, type, FF, D, blob + (size_t)FF * QE_GU_ROW_BYTES);
+    orc_nl4_quantize_rows((const uint8_t *)down + dn_src, type, D, FF, blob + QE_EXPERT_DOWN_OFF);
+    return 0;
+}

@@ -465,6 +465,65 @@ int qe_moe_profile_read(qe_moe_ctx *c, double *ms, int *launches, int n) {
 
 const char *qe_moe_profile_name(int id) { return (id >= 0 && id < QP_N) ? k_prof_names[id] : ""; }
 
+static size_t src_block_bytes(int type) {
+    switch (type) {
+    case QE_SRC_F32: return 128;
+    case QE_SRC_F16: case QE_SRC_BF16: return 64;
+    case QE_SRC_Q8_0: return 34;
+    default: return 0;
+    }
+}
+
+int qe_moe_nl4_quantize_rows(const void *src, int src_type, int64_t rows, int cols, void *dst, void *stream) {
+    if (!src || !dst || rows < 0 || cols <= 0 || cols % 256 || ((uintptr_t)src | (uintptr_t)dst) % 16)
+        return fail(QE_ERR_ARG, "nl4_quantize_rows: bad argument (rows=%lld cols=%d)", (long long)rows, cols);
+    if (!src_block_bytes(src_type)) return fail(QE_ERR_ARG, "nl4_quantize_rows: unsupported source type %d", src_type);
+    const int64_t nblk = rows * (cols / 32);
+    if (nblk >= ((int64_t)1 << 31)) return fail(QE_ERR_ARG, "nl4_quantize_rows: %lld blocks (max 2^31 - 1)", (long long)nblk);
+    QeNl4Args a;
+    a.src = (const uint8_t *)src;
+    a.dst = (uint8_t *)dst;
+    a.nblk = (uint32_t)nblk;
+    a.nb = (uint32_t)(cols / 32);
+    a.rows_per_group = rows > 0 ? (uint32_t)rows : 1u;
+    a.group_stride = 0;
+    a.row_stride = QE_NL4_ROW_BYTES(cols);
+    HIP_TRY(qe_launch_nl4_quant(a, src_type, (hipStream_t)stream));
+    return QE_OK;
+}
+
+int qe_moe_convert_experts(qe_moe_ctx *c, int layer, const void *gate, const void *up, const void *down, int src_type,
+                           void *stream) {
+    if (!c || layer < 0 || layer >= c->n_layers || !gate || !up || !down ||
+        ((uintptr_t)gate | (uintptr_t)up | (uintptr_t)down) % 16)
+        return fail(QE_ERR_ARG, "convert_experts: bad argument");
+    if (!src_block_bytes(src_type)) return fail(QE_ERR_ARG, "convert_experts: unsupported source type %d", src_type);
+    HIP_TRY(hipSetDevice(c->device));
+    uint8_t *base = c->arena + (size_t)layer * QE_LAYER_EXPERT_BYTES;
+    QeNl4Args a;
+    a.group_stride = QE_EXPERT_BYTES;
+    // gate and up: 256 x 512 rows of 64 blocks
+    a.nb = QE_D / 32;
+    a.rows_per_group = QE_FF_EXP;
+    a.nblk = QE_N_EXPERT * QE_FF_EXP * a.nb;
+    a.row_stride = QE_GU_ROW_BYTES;
+    a.src = (const uint8_t *)gate;
+    a.dst = base;
+    HIP_TRY(qe_launch_nl4_quant(a, src_type, (hipStream_t)stream));
+    a.src = (const uint8_t *)up;
+    a.dst = base + (size_t)QE_FF_EXP * QE_GU_ROW_BYTES;
+    HIP_TRY(qe_launch_nl4_quant(a, src_type, (hipStream_t)stream));
+    // down: 256 x 2048 rows of 16 blocks
+    a.nb = QE_FF_EXP / 32;
+    a.rows_per_group = QE_D;
+    a.nblk = QE_N_EXPERT * QE_D * a.nb;
+    a.row_stride = QE_DN_ROW_BYTES;
+    a.src = (const uint8_t *)down;
+    a.dst = base + QE_EXPERT_DOWN_OFF;
+    HIP_TRY(qe_launch_nl4_quant(a, src_type, (hipStream_t)stream));
+    return QE_OK;
+}
+
 int qe_moe_arena_ptr(qe_moe_ctx *c, int layer, void **dev) {
     if (!c || !dev || layer < 0 || layer >= c->n_layers) return fail(QE_ERR_ARG, "arena_ptr: bad argument");
     *dev = c->arena + (size_t)layer * QE_LAYER_EXPERT_BYTES;

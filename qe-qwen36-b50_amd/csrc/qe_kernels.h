@@ -105,6 +105,16 @@ hipError_t qe_launch_dispatch(const QeScratch &S, int T, hipStream_t st);
 hipError_t qe_launch_expert_mfma(const QeLayerPtrs &L, const QeScratch &S, int T, hipStream_t st);
 hipError_t qe_launch_router_shgu(const QeLayerPtrs &L, const QeScratch &S, int T, hipStream_t st);
 
+// IQ4_NL conversion (qe_convert.hip): block g (of nblk, nb per row) of the
+// source goes to row g / nb of the destination, rows grouped rows_per_group
+// at a time (one expert's matrix) at group_stride, row_stride within a group.
+struct QeNl4Args {
+    const uint8_t *src; uint8_t *dst;
+    uint32_t nblk, nb, rows_per_group;
+    size_t group_stride, row_stride;
+};
+hipError_t qe_launch_nl4_quant(const QeNl4Args &a, int src_type, hipStream_t st);
+
 hipError_t qe_launch_synth_layer(uint8_t *arena_l, float *router_l, uint8_t *sh_gu_l, uint8_t *sh_dn_l,
                                  float *post_norm_l, uint64_t seed, int layer, hipStream_t st);
 hipError_t qe_launch_synth_x(float *out, uint64_t seed, int inst, int64_t n, hipStream_t st);

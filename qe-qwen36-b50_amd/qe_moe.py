@@ -32,6 +32,8 @@ SH_GU_BYTES = 1024 * 2176
 SH_DN_BYTES = 2048 * 544
 
 NPROF = 11
+# ggml type ids of converter sources (QE_SRC_* in the header)
+SRC_F32, SRC_F16, SRC_Q8_0, SRC_BF16 = 0, 1, 8, 30
 QE_OK, QE_ERR_ARG, QE_ERR_HIP, QE_ERR_OOM, QE_ERR_STATE = 0, -1, -2, -3, -4
 
 
@@ -84,6 +86,8 @@ def load(path: str = LIB_PATH):
         "qe_moe_profile": (i32, [vp, i32]),
         "qe_moe_profile_read": (i32, [vp, vp, vp, i32]),
         "qe_moe_profile_name": (ctypes.c_char_p, [i32]),
+        "qe_moe_nl4_quantize_rows": (i32, [vp, i32, i64, i32, vp, vp]),
+        "qe_moe_convert_experts": (i32, [vp, i32, vp, vp, vp, i32, vp]),
     }
     for name, (res, args) in sig.items():
         f = getattr(lib, name)
@@ -156,6 +160,11 @@ class MoE:
     def load_pack(self, path, pack_first, first_layer, n_layers, stream=None):
         _check(_lib.qe_moe_load_pack(self.h, str(path).encode(), pack_first, first_layer, n_layers, _stream(stream)))
 
+    def convert_experts(self, layer, gate, up, down, src_type, stream=None):
+        """Quantize blk.N.ffn_{gate,up,down}_exps (device tensors of ggml type src_type) into the layer's arena."""
+        _check(_lib.qe_moe_convert_experts(self.h, layer, _ptr(gate), _ptr(up), _ptr(down), src_type,
+                                           _stream(stream)))
+
     def arena_ptr(self, layer) -> int:
         p = ctypes.c_void_p()
         _check(_lib.qe_moe_arena_ptr(self.h, layer, ctypes.byref(p)))
@@ -208,3 +217,9 @@ class MoE:
 def synth_x(seed, inst, dev_out, n, stream=None):
     load()
     _check(_lib.qe_moe_synth_x(seed, inst, _ptr(dev_out), n, _stream(stream)))
+
+
+def nl4_quantize_rows(src, src_type, rows, cols, dst, stream=None):
+    """rows x cols weights of ggml type src_type (device) -> NL4 rows in dst (device), on the current device."""
+    load()
+    _check(_lib.qe_moe_nl4_quantize_rows(_ptr(src), src_type, rows, cols, _ptr(dst), _stream(stream)))

@@ -25,6 +25,14 @@ def test_expert_bytes_and_argument_errors():
     assert lib.qe_moe_forward_norm(None, 0, None, None, 1, None, None, None) == qe_moe.QE_ERR_ARG
     assert lib.qe_moe_load_pack(None, b"x.pack", 0, 0, 1, None) == qe_moe.QE_ERR_ARG
     assert lib.qe_moe_destroy(None) == 0
+    # converter argument checks return before any device call
+    assert lib.qe_moe_nl4_quantize_rows(None, 8, 1, 2048, None, None) == qe_moe.QE_ERR_ARG
+    assert lib.qe_moe_nl4_quantize_rows(16, 8, 1, 100, 32, None) == qe_moe.QE_ERR_ARG
+    assert lib.qe_moe_nl4_quantize_rows(16, 8, 1, 2048, 40, None) == qe_moe.QE_ERR_ARG
+    assert lib.qe_moe_nl4_quantize_rows(16, 2, 1, 2048, 32, None) == qe_moe.QE_ERR_ARG
+    assert b"unsupported source type 2" in lib.qe_moe_last_error()
+    assert lib.qe_moe_nl4_quantize_rows(16, 8, 1 << 26, 2048, 32, None) == qe_moe.QE_ERR_ARG
+    assert lib.qe_moe_convert_experts(None, 0, 16, 32, 48, 8, None) == qe_moe.QE_ERR_ARG
 
 
 def test_missing_library_fails_loudly(tmp_path):

@@ -296,3 +296,167 @@ def test_zipf_bias_is_a_permutation_of_log_ranks():
     assert np.array_equal(ranks, np.arange(1, 257))
     b13 = O.gen_zipf_bias(SEED, 0, 1.3)
     assert np.allclose(b13, 1.3 * b, rtol=1e-6)
+
+
+# ---------------------------------------------------------------------------
+# IQ4_NL converter (ggml's quantizer as engine/qconv.cpp:91-98 calls it)
+# ---------------------------------------------------------------------------
+def _nearest_brute(a):
+    """Index of the codebook entry closest to each float32 a; equal distances go to the larger entry."""
+    a = np.asarray(a, np.float32)
+    dist = np.abs(a[:, None] - KV.astype(np.float32)[None, :])  # float32 differences, as ggml rounds them
+    return 15 - np.argmin(dist[:, ::-1], axis=1)
+
+
+def _nearest_mid(a):
+    """Count of bracket midpoints <= a (the form the GPU kernel evaluates)."""
+    mids = (KV[:-1] + KV[1:]).astype(np.float32) / np.float32(2)
+    return np.sum(np.asarray(a, np.float32)[:, None] >= mids[None, :], axis=1)
+
+
+def test_nl4_nearest_brute_force_and_midpoint_form():
+    rng = np.random.default_rng(11)
+    mids = (KV[:-1] + KV[1:]) / 2.0
+    a = [rng.uniform(-160, 160, 20000), KV, mids, [0.0, -0.0, -127.0, 113.0, -1e6, 1e6, 1e-30, -1e-30]]
+    near = [np.concatenate([np.asarray(v, np.float32) for v in a])]
+    for v in np.concatenate([mids, KV]).astype(np.float32):  # a thousand ulps either side of each
+        u = np.full(1001, v, np.float32)
+        for i in range(1, 1001):
+            u[i] = np.nextafter(u[i - 1], np.float32(np.inf))
+        w = np.full(1001, v, np.float32)
+        for i in range(1, 1001):
+            w[i] = np.nextafter(w[i - 1], np.float32(-np.inf))
+        near += [u, w]
+    a = np.concatenate(near)
+    got = np.array([O.nl4_nearest(float(v)) for v in a])
+    assert np.array_equal(got, _nearest_brute(a))
+    assert np.array_equal(got, _nearest_mid(a))
+    # ties go to the larger entry: 7 is midway between 1 and 13
+    assert O.nl4_nearest(7.0) == 9 and O.nl4_nearest(np.nextafter(np.float32(7), np.float32(0))) == 8
+
+
+def _dequant_block(d16, codes):
+    idx = np.concatenate([codes & 15, codes >> 4]).astype(np.int64)
+    return KV[idx].astype(np.float64) * float(np.array([d16], np.uint16).view(np.float16)[0])
+
+
+def test_nl4_block_exact_fit_recovers_scale_and_codes():
+    rng = np.random.default_rng(12)
+    for trial in range(200):
+        s = np.float32(2.0 ** int(rng.integers(-12, 4))) * (1 if trial % 2 else -1)
+        idx = rng.integers(0, 16, 32)
+        idx[rng.integers(0, 32)] = 0  # -127: the entry of largest magnitude fixes m
+        x = (KV[idx] * s).astype(np.float32)
+        d16, codes, d = O.nl4_block(x)
+        assert d == s and d16 == int(np.array([s], np.float16).view(np.uint16)[0])
+        assert np.array_equal(np.concatenate([codes & 15, codes >> 4]), idx), trial  # byte j: j | j+16 << 4
+        assert np.array_equal(_dequant_block(d16, codes), x.astype(np.float64))
+
+
+def _candidates(x):
+    """ggml's 16 candidate inverse scales of a block, in float32."""
+    x = np.asarray(x, np.float32)
+    j = int(np.argmax(np.abs(x)))  # first of the largest |x|
+    m = x[j]
+    s = [np.float32(1) / (m / np.float32(127))]
+    s += [np.float32(t - 127) / m for t in range(-7, 8)]
+    return s
+
+
+def _objective(x, s):
+    """Weighted least-squares fit of one candidate, in float64: (score, d)."""
+    x64 = np.asarray(x, np.float64)
+    q = KV[_nearest_brute(np.float32(s) * np.asarray(x, np.float32))].astype(np.float64)
+    w = x64 * x64
+    sxq, sqq = np.sum(w * q * x64), np.sum(w * q * q)
+    return sxq * sxq / sqq, sxq / sqq
+
+
+def test_nl4_block_picks_the_best_candidate():
+    rng = np.random.default_rng(13)
+    gens = [lambda: rng.standard_normal(32), lambda: rng.standard_t(3, 32), lambda: rng.uniform(-1, 1, 32),
+            lambda: np.where(rng.random(32) < 0.2, rng.standard_normal(32) * 20, rng.standard_normal(32))]
+    blocks = [gens[i % 4]() * 10.0 ** rng.uniform(-4, 2) for i in range(2000)]
+    for b in blocks[::8]:  # +A and -A both present: m is the first of them
+        j = int(np.argmax(np.abs(b)))
+        b[(j + 1 + int(rng.integers(0, 31))) % 32] = -b[j]
+    hist = np.zeros(16, int)
+    for x in blocks:
+        x = np.asarray(x, np.float32)
+        d16, codes, d = O.nl4_block(x)
+        objs = [_objective(x, s) for s in _candidates(x)]
+        score = np.array([o[0] for o in objs])
+        best = int(np.argmax(score))
+        hist[best] += 1
+        # the chosen fit is a best-scoring candidate's (near-ties within fp32 rounding)
+        ok = [i for i in range(16) if score[i] >= score[best] * (1 - 1e-5) and abs(objs[i][1] - d) <= 1e-5 * abs(d)]
+        assert ok, (x, d)
+        # codes are the nearest entries of x / d, and the scale is fp16(d)
+        assert d16 == int(np.array([d], np.float16).view(np.uint16)[0])
+        want = _nearest_brute(np.float32(1) / np.float32(d) * x)
+        assert np.array_equal(np.concatenate([codes & 15, codes >> 4]), want)
+    # every candidate wins somewhere, so a search that drops one fails above
+    assert (hist > 0).sum() >= 14, hist
+
+
+def test_nl4_block_zero_and_tiny():
+    d16, codes, d = O.nl4_block(np.zeros(32, np.float32))
+    assert d == 0 and d16 == 0 and np.all(codes == 0x88)  # nearest entry to 0 is 1 (index 8)
+    x = np.zeros(32, np.float32)
+    x[5] = np.float32(9e-16)  # below ggml's 1e-15 group threshold
+    assert O.nl4_block(x)[2] == 0
+    x[5] = np.float32(1e-15)  # at the threshold: quantized; the fp16 scale underflows to 0
+    d16, codes, d = O.nl4_block(x)
+    assert d > 0 and d16 == 0 and (codes[5] & 15) in (14, 15)
+
+
+def test_nl4_rows_source_types_and_layout():
+    rng = np.random.default_rng(14)
+    rows, cols = 6, 2048
+    nb = rows * cols // 32
+    # Q8_0 with power-of-two scales: every value is exact in F32, F16 and BF16 as well
+    d = (2.0 ** rng.integers(-10, -2, nb)).astype(np.float16)
+    q = rng.integers(-127, 128, (nb, 32)).astype(np.int8)
+    q8 = np.concatenate([d.view(np.uint8).reshape(nb, 2), q.view(np.uint8)], axis=1)
+    x = (d.astype(np.float32)[:, None] * q.astype(np.float32)).reshape(rows, cols)
+    ref = O.nl4_quantize_rows(x, O.SRC_F32, rows, cols)
+    assert np.array_equal(O.nl4_quantize_rows(q8, O.SRC_Q8_0, rows, cols), ref)
+    assert np.array_equal(O.nl4_quantize_rows(x.astype(np.float16), O.SRC_F16, rows, cols), ref)
+    bf = (x.view(np.uint32) >> 16).astype(np.uint16)
+    assert np.array_equal((bf.astype(np.uint32) << 16).view(np.float32), x)
+    assert np.array_equal(O.nl4_quantize_rows(bf, O.SRC_BF16, rows, cols), ref)
+    # Q8_0 with arbitrary fp16 scales decodes as fp32(d) * q
+    d2 = (rng.random(nb) * 0.01).astype(np.float16)
+    q8b = np.concatenate([d2.view(np.uint8).reshape(nb, 2), q.view(np.uint8)], axis=1)
+    xb = (d2.astype(np.float32)[:, None] * q.astype(np.float32)).reshape(rows, cols)
+    assert np.array_equal(O.nl4_quantize_rows(q8b, O.SRC_Q8_0, rows, cols), O.nl4_quantize_rows(xb, O.SRC_F32, rows, cols))
+    # row layout = the one the inference path reads: the NL4 dot of a quantized row
+    # against int8 activations equals the float64 dot of its dequantized values
+    xa = rng.standard_normal(cols).astype(np.float32)
+    xq, xs = O.quant_x(xa)
+    act = (xq.astype(np.float64).reshape(-1, 32) * xs.astype(np.float64)[:, None]).reshape(-1)
+    deq = O.nl4_dequant_rows(ref, cols).astype(np.float64)
+    for r in range(rows):
+        got = O.dot_nl4(ref[r], cols, xq, xs)
+        assert abs(got - deq[r] @ act) <= 1e-4 * np.abs(deq[r] * act).sum()
+    # 4-bit error level of the non-uniform codebook on Gaussian rows
+    g = rng.standard_normal((64, cols)).astype(np.float32)
+    e = np.linalg.norm(O.nl4_dequant_rows(O.nl4_quantize_rows(g, O.SRC_F32, 64, cols), cols) - g) / np.linalg.norm(g)
+    assert 0.05 < e < 0.12, e
+
+
+def test_convert_expert_row_placement():
+    rng = np.random.default_rng(15)
+    e = 1  # the oracle reads only expert e's slice, so two experts' worth of source suffice
+    n_gu, n_dn = 2 * 512 * 2048 // 32, 2 * 2048 * 512 // 32
+
+    def q8(n):
+        d = (rng.random(n) * 0.02).astype(np.float16)
+        return np.concatenate([d.view(np.uint8).reshape(n, 2), rng.integers(0, 256, (n, 32), dtype=np.uint8)], 1)
+
+    gate, up, down = q8(n_gu), q8(n_gu), q8(n_dn)
+    blob = O.convert_expert(gate, up, down, O.SRC_Q8_0, e)
+    half_gu, half_dn = n_gu // 2, n_dn // 2
+    assert np.array_equal(blob[:512 * 1152], O.nl4_quantize_rows(gate[half_gu:], O.SRC_Q8_0, 512, 2048).reshape(-1))
+    assert np.array_equal(blob[512 * 1152:1024 * 1152], O.nl4_quantize_rows(up[half_gu:], O.SRC_Q8_0, 512, 2048).reshape(-1))
+    assert np.array_equal(blob[1024 * 1152:], O.nl4_quantize_rows(down[half_dn:], O.SRC_Q8_0, 2048, 512).reshape(-1))
