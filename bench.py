@@ -12,6 +12,10 @@ HBM arena, inputs resident in HBM before timing.  Also reported:
   * prefill8192_zipf13: BASELINE config 4 (8192 tokens, one layer, Zipf s=1.3),
     472.5 GFLOP per call / time;
   * decode_b8: 8 tokens per step through the 40-layer stack;
+  * convert_layer_q8_0: the IQ4_NL converter, one layer's routed experts
+    (blk.N.ffn_{gate,up,down}_exps in Q8_0, the reference converter's input)
+    quantized into the arena, against the CPU restatement of ggml's quantizer
+    on a few experts (--convert-only runs just this, for profiling);
   * roofline: the decode kernel (k_decode, the only kernel of a decode step)
     timed with the library's HIP events on the launch stream over a profiled
     pass of the same workload;
@@ -93,6 +97,47 @@ def cpu_baseline(n_distinct, budget_s, max_tokens, threads):
     return tokens / total, total, tokens
 
 
+CONVERT_SRC_BYTES = 3 * 256 * 1048576 // 32 * 34  # Q8_0 gate, up, down of one layer
+CONVERT_DST_BYTES = 256 * EXPERT_BYTES
+
+
+def convert_bench(torch, qe_moe, steps, cpu_experts, threads):
+    """One layer of Q8_0 experts -> arena blobs (qe_moe_convert_experts), HIP events on the launch stream."""
+    g = torch.Generator(device="cuda")
+    g.manual_seed(SEED)
+
+    def q8(nblk):
+        t = torch.randint(0, 256, (nblk, 34), dtype=torch.uint8, device="cuda", generator=g)
+        t[:, :2] = (torch.rand(nblk, device="cuda", generator=g) * 0.02).half().view(torch.uint8).view(nblk, 2)
+        return t
+
+    gate, up, down = q8(256 * 512 * 64), q8(256 * 512 * 64), q8(256 * 2048 * 16)
+    m = qe_moe.MoE(n_layers=1, t_max=16)
+    st = torch.cuda.current_stream()
+    run = lambda: m.convert_experts(0, gate, up, down, qe_moe.SRC_Q8_0, stream=st)  # noqa: E731
+    run()
+    ms = timed(torch, run, steps, st)
+    res = {"ms": round(ms, 4), "blocks": 3 * 256 * 1048576 // 32,
+           "algorithmic_bytes": CONVERT_SRC_BYTES + CONVERT_DST_BYTES,
+           "gbs": round((CONVERT_SRC_BYTES + CONVERT_DST_BYTES) / (ms / 1e3) / 1e9, 1),
+           "hbm_frac": round((CONVERT_SRC_BYTES + CONVERT_DST_BYTES) / (ms / 1e3) / HBM_PEAK, 4),
+           "bound": "valu (16 candidate scales x 32 elements per block, exact fp32 order)"}
+    if cpu_experts:
+        sys.path.insert(0, os.path.join(REPO, "oracle"))
+        import oracle as O
+
+        hg, hu, hd = (t.cpu().numpy() for t in (gate, up, down))
+        O.load().orc_set_threads(threads)
+        t0 = time.perf_counter()
+        for e in range(cpu_experts):
+            O.convert_expert(hg, hu, hd, O.SRC_Q8_0, e)
+        cs = time.perf_counter() - t0
+        res["cpu_baseline"] = {"ms_per_layer": round(cs / cpu_experts * 256 * 1e3, 1), "cores": threads, "kind": "port",
+                               "sample": f"{cpu_experts} experts of the same layer, scaled to 256"}
+    m.close()
+    return res
+
+
 def pmc_traffic(path):
     """HBM bytes per k_decode dispatch from the committed rocprofv3 --pmc summary
     (FETCH_SIZE and WRITE_SIZE in KiB per dispatch, each divided by the factor
@@ -126,6 +171,8 @@ def main():
     ap.add_argument("--cpu-layers", type=int, default=8, help="distinct synthetic layers cycled by the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="timed CPU work of the baseline sample")
     ap.add_argument("--cpu-threads", type=int, default=16, help="host threads of the CPU baseline (the box's CPU share)")
+    ap.add_argument("--no-convert", action="store_true", help="skip the IQ4_NL converter side line")
+    ap.add_argument("--convert-only", action="store_true", help="run only the converter side line (profiling)")
     ap.add_argument("--copy-bytes", type=int, default=0,
                     help="only run a plain device copy of this many bytes 5 times (PMC calibration) and exit")
     args = ap.parse_args()
@@ -148,6 +195,11 @@ def main():
         return
 
     import qe_moe
+
+    threads = max(1, min(os.cpu_count() or 1, args.cpu_threads))
+    if args.convert_only:
+        print(json.dumps({"convert_layer_q8_0": convert_bench(torch, qe_moe, 5, 0, threads)}), flush=True)
+        return
 
     stream = torch.cuda.current_stream()
 
@@ -297,10 +349,15 @@ def main():
         del m4, x4, y4
         torch.cuda.empty_cache()
 
+    conv = None
+    if not args.no_convert:
+        log("converter: one layer of Q8_0 experts")
+        conv = convert_bench(torch, qe_moe, 5, 0 if args.no_cpu_baseline else 4, threads)
+        torch.cuda.empty_cache()
+
     # ---------------- CPU baseline ----------------
     cpu = None
     if not args.no_cpu_baseline:
-        threads = max(1, min(os.cpu_count() or 1, args.cpu_threads))
         log(f"cpu baseline: {args.cpu_layers} distinct layers cycled over 40 steps, ~{args.cpu_seconds} s, {threads} threads")
         cpu_tok_s, cpu_sec, cpu_tok = cpu_baseline(args.cpu_layers, args.cpu_seconds, 100000, threads)
         cpu = {"value": round(cpu_tok_s, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
@@ -333,6 +390,7 @@ def main():
                      "avg_us": round(dec_avg_s * 1e6, 3)},
         "kernels": kernels,
         "decode_b8": decode_b8,
+        "convert_layer_q8_0": conv,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

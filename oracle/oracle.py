@@ -68,6 +68,7 @@ def load():
         "orc_nl4_block": (f32, [vp, vp, vp]),
         "orc_nl4_quantize_rows": (i32, [vp, i32, i64, i32, vp]),
         "orc_convert_expert": (i32, [vp, vp, vp, i32, i32, vp]),
+        "orc_set_threads": (None, [i32]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)

@@ -568,6 +568,9 @@ ORC_API int orc_nl4_quantize_rows(const void *src, int type, int64_t rows, int c
     return 0;
 }
 
+/* OpenMP threads of the calling thread's later parallel regions. */
+ORC_API void orc_set_threads(int n) { omp_set_num_threads(n); }
+
 /* Expert e's blob from the layer's ffn_{gate,up,down}_exps tensors. */
 ORC_API int orc_convert_expert(const void *gate, const void *up, const void *down, int type, int e, uint8_t *blob) {
     const size_t bb = (size_t)src_block_bytes(type);
