@@ -17,58 +17,70 @@
 // Here one thread quantizes one block, with the fp32 operations of that
 // sequence in the same order (the library builds with -ffp-contract=off and
 // correctly rounded division), so the bytes are identical to the CPU
-// checker's.  The work is VALU-bound: 16 candidates x 32 elements, about 13
-// instructions each, against 1.6 bytes of HBM traffic per element.
+// checker's.  The work is VALU-bound: 16 candidates x 32 elements against
+// 1.6 bytes of HBM traffic per element.
 //
 // nearest(a): ggml bisects the codebook and keeps the lower of the two
 // bracketing entries when a - lo < hi - a.  Both differences are exact
 // wherever the comparison is close (every midpoint lies at |a| >= 4.5 and the
-// entries are integers), so that test is a < (lo + hi)/2.  A 241-entry LDS
-// table indexed by floor(a), clamped to [-127, 113], holds {mid, lo} of the
-// bracket containing [k, k+1); hi = 2*mid - lo.  Past the last entry mid is
-// 1e30, so a >= 113 keeps 113; below -127 the first bracket keeps -127.
+// entries are integers), so that test is a < (lo + hi)/2.  The brackets have
+// integer ends and the midpoints are multiples of 1/2, so nearest(a) is
+// constant on every half-unit slot [k/2, (k+1)/2): one LDS table of the slot
+// values answers it.  The slot comes from 8a, whose floor rounded down to a
+// multiple of 4 is the byte offset 4 floor(2a) of a 4-byte entry; 8a is exact
+// (a power-of-two scaling), so it is 8 times the a that ggml rounds.
+//
+// In the candidate loop |a| <= |s m| <= 134.02 (|x_j| <= |m|, |s| <= 134/|m|)
+// or a is NaN (a NaN or infinite input; v_cvt_flr_i32_f32 gives 0), so the
+// table spans a in [-135.5, 135.5) and needs no clamp there.  The final pass
+// uses s = 1/d, which has no such bound, and clamps.
 #include "../../include/qe_moe.h"
 #include "qe_kernels.h"
 
 namespace {
 
-constexpr int NL4_TAB = 241; // k = -127 .. 113
+constexpr int NL4_HALF = 271;          // slots k = -271 .. 270
+constexpr int NL4_SLOTS = 2 * NL4_HALF; // 542 entries
 
 __device__ inline int kv_at(int i) {
     const uint32_t w = i < 4 ? QE_NL4_W0 : i < 8 ? QE_NL4_W1 : i < 12 ? QE_NL4_W2 : QE_NL4_W3;
     return (int)(int8_t)(w >> (8 * (i & 3)));
 }
 
-__device__ inline void build_table(float2 *tab, int *tab_lo) {
-    for (int t = threadIdx.x; t < NL4_TAB; t += blockDim.x) {
-        const int k = t - 127;
+// slot k holds a in [k/2, (k+1)/2): value and index of the nearest entry
+__device__ inline void build_table(float *tab_q, int *tab_c) {
+    for (int t = threadIdx.x; t < NL4_SLOTS; t += blockDim.x) {
+        const int k = t - NL4_HALF;
+        const int fl = k >> 1; // floor(a)
         int lo = 0;
         for (int i = 1; i < 16; ++i)
-            if (kv_at(i) <= k) lo = i;
-        const float vlo = (float)kv_at(lo);
-        const float mid = lo < 15 ? 0.5f * (vlo + (float)kv_at(lo + 1)) : 1e30f;
-        tab[t] = make_float2(mid, vlo);
-        tab_lo[t] = lo;
+            if (kv_at(i) <= fl) lo = i;
+        // a < (v_lo + v_hi)/2  <=>  k + 1/2 < v_lo + v_hi  <=>  k < v_lo + v_hi
+        const int c = lo < 15 && k >= kv_at(lo) + kv_at(lo + 1) ? lo + 1 : lo;
+        tab_q[t] = (float)kv_at(c);
+        tab_c[t] = c;
     }
 }
 
-// table slot of a: floor(a) clamped to [-127, 113], + 127 (NaN -> 0); one
-// v_cvt_flr_i32_f32 in place of the floor + convert pair the compiler emits
-__device__ inline int tab_slot(float a) {
+// byte offset of the slot of a, from a8 = 8a: 4 floor(2a) = floor(a8) & ~3
+__device__ inline int slot_bytes(float a8) {
     int k;
-    asm("v_cvt_flr_i32_f32 %0, %1" : "=v"(k) : "v"(fminf(fmaxf(a, -127.f), 113.f)));
-    return k + 127;
+    asm("v_cvt_flr_i32_f32 %0, %1" : "=v"(k) : "v"(a8));
+    return k & ~3;
 }
 
-// S_xq and S_qq of inverse scale s, in element order
-__device__ inline void nl4_fit(const float (&x)[32], float s, const float2 *tab, float &sxq, float &sqq) {
+template <typename T> __device__ inline T tab_at(const T *tab0, int bytes) {
+    return *(const T *)((const char *)tab0 + bytes);
+}
+
+// S_xq and S_qq of inverse scale s (given as s8 = 8 s), in element order
+__device__ inline void nl4_fit(const float (&x)[32], const float (&w)[32], float s8, const float *tab0, float &sxq,
+                               float &sqq) {
     float a = 0.f, b = 0.f;
 #pragma unroll
     for (int j = 0; j < 32; ++j) {
-        const float al = s * x[j];
-        const float2 e = tab[tab_slot(al)];
-        const float q = al < e.x ? e.y : fmaf(2.f, e.x, -e.y);
-        const float wq = (x[j] * x[j]) * q;
+        const float q = tab_at(tab0, slot_bytes(s8 * x[j]));
+        const float wq = w[j] * q;
         a = a + wq * x[j];
         b = b + wq * q;
     }
@@ -116,41 +128,44 @@ __device__ inline void load_block(const uint8_t *src, uint32_t g, float (&x)[32]
 
 template <int TYPE>
 __global__ __launch_bounds__(256) void k_nl4_quant(QeNl4Args a) {
-    __shared__ float2 s_tab[NL4_TAB];
-    __shared__ int s_lo[NL4_TAB];
-    build_table(s_tab, s_lo);
+    __shared__ float s_q[NL4_SLOTS];
+    __shared__ int s_c[NL4_SLOTS];
+    build_table(s_q, s_c);
     __syncthreads();
     const uint32_t g = blockIdx.x * 256u + threadIdx.x;
     if (g >= a.nblk) return;
-    float x[32];
+    float x[32], w[32];
     load_block<TYPE>(a.src, g, x);
+    const float *q0 = s_q + NL4_HALF;
 
     float amax = 0.f, m = 0.f;
 #pragma unroll
-    for (int j = 0; j < 32; ++j)
+    for (int j = 0; j < 32; ++j) {
+        w[j] = x[j] * x[j];
         if (fabsf(x[j]) > amax) { amax = fabsf(x[j]); m = x[j]; }
+    }
     float d = 0.f;
     if (amax >= 1e-15f) {
         float sxq, sqq;
-        nl4_fit(x, 1.f / (m / 127.f), s_tab, sxq, sqq);
+        nl4_fit(x, w, 8.f * (1.f / (m / 127.f)), q0, sxq, sqq);
         d = sxq / sqq;
         float best = d * sxq;
 #pragma unroll 1
         for (int t = -7; t <= 7; ++t) {
-            nl4_fit(x, (float)(t - 127) / m, s_tab, sxq, sqq);
+            nl4_fit(x, w, 8.f * ((float)(t - 127) / m), q0, sxq, sqq);
             if (sqq > 0.f && sxq * sxq > best * sqq) {
                 d = sxq / sqq;
                 best = d * sxq;
             }
         }
     }
-    const float s = d != 0.f ? 1.f / d : 0.f;
+    const float s8 = 8.f * (d != 0.f ? 1.f / d : 0.f);
+    const int *c0 = s_c + NL4_HALF;
     uint32_t c[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
     for (int j = 0; j < 32; ++j) {
-        const float al = s * x[j];
-        const int slot = tab_slot(al);
-        const uint32_t code = (uint32_t)s_lo[slot] + (al < s_tab[slot].x ? 0u : 1u);
+        const float a8 = fminf(fmaxf(s8 * x[j], -1080.f), 1079.f); // NaN -> -1080
+        const uint32_t code = (uint32_t)tab_at(c0, slot_bytes(a8));
         c[(j & 15) >> 2] |= code << (8 * (j & 3) + (j >> 4) * 4);
     }
     const uint32_t row = g / a.nb, b = g - row * a.nb;
