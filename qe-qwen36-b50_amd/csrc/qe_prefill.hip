@@ -632,34 +632,64 @@ QE_DEV void shgu_tile(const _Float16 *xhl, int T, const uint8_t *W, _Float16 *hh
 }
 
 
-// Router split tiles and shared gate/up tiles in one launch, interleaved
-// (even workgroups route, odd ones run the shared expert while both kinds
-// remain), so the fp32 VALU router and the matrix-core shared GEMM share the
-// CUs instead of running back to back.
+// Router split tiles and shared gate/up tiles in one launch, so the fp32 VALU
+// router and the matrix-core shared GEMM share the CUs instead of running back
+// to back.  Workgroup b runs on XCD b % 8 (the dispatcher deals workgroups
+// round robin over the 8 XCDs, each with its own L2), and the tasks are dealt
+// so that every XCD gets both kinds, interleaved, and the tiles that share an
+// operand run on one XCD back to back: the 4 router column tiles of one
+// (token tile, K split) and the 16 shared gate/up row tiles of one token tile.
+constexpr int RS_NT = QE_N_EXPERT / 64, RS_JT = QE_FF_SH / 32;
+QE_DEV int rs_router_per_xcd(int T) { return RS_NT * ((T + 63) / 64) * RT_SPLIT / 8; }
+QE_DEV int rs_shgu_per_xcd(int T, int x) { return RS_JT * (((T + 31) / 32 - x + 7) / 8); }
 __global__ __launch_bounds__(256) void k_router_shgu(const float *xn, const _Float16 *xhl, int T, const float *Wr,
                                                      const uint8_t *Wg, float *part, _Float16 *hhl) {
     __shared__ union {
         RouterSmem r;
         ShguSmem s;
     } sm;
+    static_assert(RT_SPLIT % 8 == 0, "router groups divide evenly over the XCDs");
+    const int x = blockIdx.x & 7, k = blockIdx.x >> 3;
     const int mt64 = (T + 63) / 64, mt32 = (T + 31) / 32;
-    const int nr = (QE_N_EXPERT / 64) * mt64 * RT_SPLIT, ns = mt32 * (QE_FF_SH / 32);
-    const int b = blockIdx.x, both = 2 * (nr < ns ? nr : ns);
+    const int nr = rs_router_per_xcd(T), ns = rs_shgu_per_xcd(T, x), both = 2 * (nr < ns ? nr : ns);
     bool router;
     int idx;
-    if (b < both) {
-        router = (b & 1) == 0;
-        idx = b >> 1;
+    if (k < both) {
+        router = (k & 1) == 0;
+        idx = k >> 1;
     } else {
         router = nr > ns;
-        idx = b - both + (both >> 1);
+        idx = k - both + (both >> 1);
     }
     if (router) {
-        const int n_tile = idx % (QE_N_EXPERT / 64), rest = idx / (QE_N_EXPERT / 64);
-        router_tile(xn, T, Wr, part, n_tile, rest % mt64, rest / mt64, sm.r);
+        if (idx >= nr) return;
+        const int g = 8 * (idx / RS_NT) + x; // (token tile, K split) group
+        router_tile(xn, T, Wr, part, idx % RS_NT, g % mt64, g / mt64, sm.r);
     } else {
-        shgu_tile(xhl, T, Wg, hhl, idx % mt32, idx / mt32, sm.s);
+        if (idx >= ns) return;
+        shgu_tile(xhl, T, Wg, hhl, 8 * (idx / RS_JT) + x, idx % RS_JT, sm.s);
     }
+    (void)mt32;
+}
+
+// From QE_RS_SPLIT_T tokens on, the two kinds run as two launches instead: the
+// shared gate/up tiles hold 128 AGPRs, which caps the fused kernel at 2 waves
+// per SIMD, while the router tiles alone (128 VGPRs) run 4.  One wave issues a
+// VALU instruction only every ~5 cycles, so the fp32 router needs the waves
+// (8192 tokens: fused 266 us; router 117 + shared 131 us).  At 512 tokens the
+// fused launch is 9 us faster (20 against 17 + 12).
+#define QE_RS_SPLIT_T 2048
+__global__ __launch_bounds__(256) void k_router(const float *xn, int T, const float *Wr, float *part) {
+    __shared__ RouterSmem sm;
+    const int x = blockIdx.x & 7, k = blockIdx.x >> 3, mt64 = (T + 63) / 64;
+    const int g = 8 * (k / RS_NT) + x;
+    router_tile(xn, T, Wr, part, k % RS_NT, g % mt64, g / mt64, sm);
+}
+__global__ __launch_bounds__(256) void k_shgu(const _Float16 *xhl, int T, const uint8_t *Wg, _Float16 *hhl) {
+    __shared__ ShguSmem sm;
+    const int x = blockIdx.x & 7, k = blockIdx.x >> 3, m = 8 * (k / RS_JT) + x;
+    if (m >= (T + 31) / 32) return;
+    shgu_tile(xhl, T, Wg, hhl, m, k % RS_JT, sm);
 }
 
 QE_DEV void shdn_tile(const _Float16 *hhl, int T, const uint8_t *W, float *out, int m_tile, int n_tile) {
@@ -717,8 +747,13 @@ __global__ __launch_bounds__(256, 2) void k_expert_dn(GemmTileArgs a, int nr, co
 }
 
 hipError_t qe_launch_router_shgu(const QeLayerPtrs &L, const QeScratch &S, int T, hipStream_t st) {
-    const int nr = (QE_N_EXPERT / 64) * ((T + 63) / 64) * RT_SPLIT, ns = ((T + 31) / 32) * (QE_FF_SH / 32);
-    k_router_shgu<<<nr + ns, 256, 0, st>>>(S.xn, S.xhl, T, L.router, L.sh_gu, S.rpart, (_Float16 *)S.shgu);
+    const int nr = RS_NT * ((T + 63) / 64) * RT_SPLIT, ns = 8 * RS_JT * (((T + 31) / 32 + 7) / 8);
+    if (T >= QE_RS_SPLIT_T) {
+        k_router<<<nr, 256, 0, st>>>(S.xn, T, L.router, S.rpart);
+        k_shgu<<<ns, 256, 0, st>>>(S.xhl, T, L.sh_gu, (_Float16 *)S.shgu);
+    } else {
+        k_router_shgu<<<nr + ns, 256, 0, st>>>(S.xn, S.xhl, T, L.router, L.sh_gu, S.rpart, (_Float16 *)S.shgu);
+    }
     return hipGetLastError();
 }
 
