@@ -107,7 +107,6 @@ template <bool GU> struct ExpertSmem {
     static constexpr int SIZE = qe_cmax(TileLds<GU, 2, 4>::SIZE, qe_cmax(TileLds<GU, 2, 2>::SIZE, TileLds<GU, 2, 1>::SIZE));
     alignas(16) uint8_t raw[SIZE];
     int pair[QE_MFMA_MC];
-    float amax[GU ? 4 : 1][QE_MFMA_MC]; // gate/up with NC = 2: each wave's |h| maximum per pair
 };
 
 // Wave = NC column groups of 16 weight rows x NT 16-pair tiles (NC MFMAs per
@@ -353,6 +352,10 @@ __device__ __forceinline__ void expert_tile(const GemmTileArgs &a, const int4 it
     } else if constexpr (GU) {
         // h rows 16 (4 yb + wv) + n: half (wv & 1) of 32-block jb
         const int jb = yb * 2 + (wv >> 1), half = wv & 1;
+        // each wave's |h| maximum per pair, in the activation stage the last turn
+        // did not read (its last reader passed the barrier that ended turn NCH - 2)
+        float(*amax)[QE_MFMA_MC] = (float(*)[QE_MFMA_MC])(sm.raw + LY::ACT + (NCH & 1) * LY::ACT_SZ);
+        static_assert(4 * QE_MFMA_MC * 4 <= LY::ACT_SZ, "maxima fit one stage");
         float h[NT][4], m[NT][4];
 #pragma unroll
         for (int t = 0; t < NT; ++t)
@@ -360,7 +363,7 @@ __device__ __forceinline__ void expert_tile(const GemmTileArgs &a, const int4 it
             for (int i = 0; i < 4; ++i) {
                 h[t][i] = silu_mul(acc[0][t][i], acc[1][t][i]);
                 m[t][i] = max16(fabsf(h[t][i]));
-                if (n == 0) sm.amax[wv][16 * t + 4 * g + i] = m[t][i];
+                if (n == 0) amax[wv][16 * t + 4 * g + i] = m[t][i];
             }
         __syncthreads();
 #pragma unroll
@@ -368,7 +371,7 @@ __device__ __forceinline__ void expert_tile(const GemmTileArgs &a, const int4 it
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 float d;
-                const float id = quant_scale_inv(fmaxf(m[t][i], sm.amax[wv ^ 1][16 * t + 4 * g + i]), d);
+                const float id = quant_scale_inv(fmaxf(m[t][i], amax[wv ^ 1][16 * t + 4 * g + i]), d);
                 const int p = s_pair[16 * t + 4 * g + i];
                 if (p >= 0) {
                     int8_t *hrow = a.hq + (size_t)p * QE_FF_EXP + (jb >> 1) * 64 + (n >> 2) * 16 + (jb & 1) * 8 + (n & 3);
