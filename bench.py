@@ -121,7 +121,7 @@ def convert_bench(torch, qe_moe, steps, cpu_experts, threads):
            "algorithmic_bytes": CONVERT_SRC_BYTES + CONVERT_DST_BYTES,
            "gbs": round((CONVERT_SRC_BYTES + CONVERT_DST_BYTES) / (ms / 1e3) / 1e9, 1),
            "hbm_frac": round((CONVERT_SRC_BYTES + CONVERT_DST_BYTES) / (ms / 1e3) / HBM_PEAK, 4),
-           "bound": "valu (16 candidate scales x 32 elements per block, exact fp32 order)"}
+           "bound": "lds (bank conflicts of the nearest-entry slot reads: 16 candidate scales x 32 elements per block)"}
     if cpu_experts:
         sys.path.insert(0, os.path.join(REPO, "oracle"))
         import oracle as O
