@@ -688,11 +688,99 @@ __global__ __launch_bounds__(256) void k_router(const float *xn, int T, const fl
     const int g = 8 * (k / RS_NT) + x;
     router_tile(xn, T, Wr, part, k % RS_NT, g % mt64, g / mt64, sm);
 }
+// Shared gate/up for large T: workgroup = 64 tokens (two 32-token tiles) x 64
+// gate rows + the same 64 up rows; wave w takes token tile w & 1 and rows
+// 32 (w >> 1) + 0..31 of both, over the full K, so no partial sums meet.  Each
+// 32-block of K, the workgroup stages the 8 KB of activations and 4 KB of Q8
+// rows in LDS once (double-buffered, one barrier per block) and every wave reads
+// its operands from there: each fetched byte feeds two waves' MFMAs instead of
+// one.  The Q8 block scales of the 128 rows sit in LDS for the whole K, block-
+// major, so the 32 rows a wave reads for one block are consecutive.
+struct Shgu64Smem {
+    alignas(16) uint8_t a[2][2][4096]; // [stage][token tile][32-block of hi|lo halves, qe_hl_off order]
+    alignas(16) uint8_t w[2][128][32]; // [stage][row: gate 0..63, up 64..127][32 int8]
+    _Float16 sc[QE_D / 32][128];       // [block][row]
+};
+QE_DEV void shgu_tile64(const _Float16 *xhl, int T, const uint8_t *W, _Float16 *hhl, int mp, int jg, Shgu64Smem &sm) {
+    constexpr uint32_t RB = QE_SH_GU_ROW_BYTES;
+    constexpr int NB = QE_D / 32;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, c = lane & 31, kh = lane >> 5;
+    const int mt32 = (T + 31) / 32, j0 = jg * 64;
+    const __amdgpu_buffer_rsrc_t ra =
+        __builtin_amdgcn_make_buffer_rsrc((void *)xhl, (short)0, mt32 * 32 * QE_D * 4, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void *)W, (short)0, (int)QE_SH_GU_BYTES, 0x00020000);
+    auto row_off = [&](int r) -> uint32_t { return (uint32_t)((r < 64 ? 0 : QE_FF_SH - 64) + j0 + r) * RB; };
+    // block scales of the 128 rows: thread (row tid / 2, half tid & 1) brings 32 of them
+    {
+        const int r = tid >> 1, h = tid & 1;
+        qe_u32x4 s[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s[i] = sh_ld(rw, row_off(r) + QE_D + 64 * h + 16 * i);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const uint32_t v = s[i][e >> 1];
+                sm.sc[32 * h + 8 * i + e][r] = __builtin_bit_cast(_Float16, (uint16_t)((e & 1) ? v >> 16 : v & 0xffffu));
+            }
+    }
+    // staging roles: chunks tid, tid + 256 (activations of token tile 0, 1), tid + 512 (rows)
+    uint32_t a_src[2];
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+        const int mt = 2 * mp + s < mt32 ? 2 * mp + s : mt32 - 1; // a tile past T reads the last one; never stored
+        a_src[s] = (uint32_t)mt * NB * 4096 + 16 * tid;
+    }
+    const int wr = tid >> 1, wh = tid & 1;
+    const uint32_t w_src = row_off(wr) + 16 * wh;
+    qe_u32x4 st[3];
+    auto fetch = [&](int b) {
+        st[0] = sh_ld(ra, a_src[0] + 4096 * b);
+        st[1] = sh_ld(ra, a_src[1] + 4096 * b);
+        st[2] = sh_ld(rw, w_src + 32 * b);
+    };
+    auto put = [&](int s) {
+        *(qe_u32x4 *)&sm.a[s][0][16 * tid] = st[0];
+        *(qe_u32x4 *)&sm.a[s][1][16 * tid] = st[1];
+        *(qe_u32x4 *)&sm.w[s][wr][16 * wh] = st[2];
+    };
+    fetch(0);
+    put(0);
+    __syncthreads();
+    const int ms = wv & 1, rg = 32 * (wv >> 1) + c, ru = 64 + rg;
+    qe_float16v ag = {}, au = {};
+#pragma unroll 2
+    for (int b = 0; b < NB; ++b) {
+        const int s = b & 1;
+        if (b + 1 < NB) fetch(b + 1);
+        qe_u32x4 a[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) a[q] = *(const qe_u32x4 *)&sm.a[s][ms][1024 * q + 16 * lane];
+        const qe_u32x4 wg = *(const qe_u32x4 *)&sm.w[s][rg][16 * kh], wu = *(const qe_u32x4 *)&sm.w[s][ru][16 * kh];
+        sh_block(a, wg, (float)sm.sc[b][rg], ag);
+        sh_block(a, wu, (float)sm.sc[b][ru], au);
+        if (b + 1 < NB) put(s ^ 1); // stage s ^ 1 was last read in block b - 1, before the barrier
+        __syncthreads();
+    }
+    const int m0 = 64 * mp + 32 * ms, j = j0 + 32 * (wv >> 1) + c;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int m = m0 + 8 * (i >> 2) + 4 * kh + (i & 3);
+        if (m < T) {
+            const float h = silu_mul(ag[i], au[i]);
+            const _Float16 hi = (_Float16)h, lo = (_Float16)(h - (float)hi);
+            uint8_t *dst = (uint8_t *)hhl + qe_hl_off(QE_FF_SH, m, j);
+            *(_Float16 *)dst = hi;
+            *(_Float16 *)(dst + QE_HL_LO) = lo;
+        }
+    }
+}
+// workgroup b on XCD b % 8: the 8 row groups of one 64-token pair back to back there
 __global__ __launch_bounds__(256) void k_shgu(const _Float16 *xhl, int T, const uint8_t *Wg, _Float16 *hhl) {
-    __shared__ ShguSmem sm;
-    const int x = blockIdx.x & 7, k = blockIdx.x >> 3, m = 8 * (k / RS_JT) + x;
-    if (m >= (T + 31) / 32) return;
-    shgu_tile(xhl, T, Wg, hhl, m, k % RS_JT, sm);
+    __shared__ Shgu64Smem sm;
+    const int x = blockIdx.x & 7, k = blockIdx.x >> 3, mp = 8 * (k / 8) + x;
+    if (mp >= (T + 63) / 64) return;
+    shgu_tile64(xhl, T, Wg, hhl, mp, k % 8, sm);
 }
 
 QE_DEV void shdn_tile(const _Float16 *hhl, int T, const uint8_t *W, float *out, int m_tile, int n_tile) {
@@ -753,7 +841,7 @@ hipError_t qe_launch_router_shgu(const QeLayerPtrs &L, const QeScratch &S, int T
     const int nr = RS_NT * ((T + 63) / 64) * RT_SPLIT, ns = 8 * RS_JT * (((T + 31) / 32 + 7) / 8);
     if (T >= QE_RS_SPLIT_T) {
         k_router<<<nr, 256, 0, st>>>(S.xn, T, L.router, S.rpart);
-        k_shgu<<<ns, 256, 0, st>>>(S.xhl, T, L.sh_gu, (_Float16 *)S.shgu);
+        k_shgu<<<64 * (((T + 63) / 64 + 7) / 8), 256, 0, st>>>(S.xhl, T, L.sh_gu, (_Float16 *)S.shgu);
     } else {
         k_router_shgu<<<nr + ns, 256, 0, st>>>(S.xn, S.xhl, T, L.router, L.sh_gu, S.rpart, (_Float16 *)S.shgu);
     }
