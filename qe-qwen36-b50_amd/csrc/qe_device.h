@@ -138,11 +138,6 @@ QE_DEV float max32(float v) {
     rows16(__float_as_uint(max16(v)), a, b);
     return fmaxf(__uint_as_float(a), __uint_as_float(b));
 }
-QE_DEV float wave_max(float v) {
-    unsigned a, b;
-    rows32(__float_as_uint(max32(v)), a, b);
-    return fmaxf(__uint_as_float(a), __uint_as_float(b));
-}
 // u32 maximum over the wave; the DPP moves use bound_ctrl (every source lane
 // exists in these patterns) so they can fold into the v_max_u32 that uses them.
 template <int CTRL> QE_DEV unsigned dpp_ub(unsigned v) {
@@ -171,23 +166,6 @@ QE_DEV unsigned wave_min_u32(unsigned v) {
     v = umin32(a, b);
     rows32(v, a, b);
     return umin32(a, b);
-}
-QE_DEV uint64_t umax64(uint64_t a, uint64_t b) { return a > b ? a : b; }
-template <int CTRL> QE_DEV uint64_t dpp64(uint64_t v) {
-    return ((uint64_t)dpp_u<CTRL>((unsigned)(v >> 32)) << 32) | dpp_u<CTRL>((unsigned)v);
-}
-QE_DEV uint64_t wave_max_u64(uint64_t v) {
-    v = umax64(v, dpp64<QE_DPP_XOR1>(v));
-    v = umax64(v, dpp64<QE_DPP_XOR2>(v));
-    v = umax64(v, dpp64<QE_DPP_HMIRROR>(v));
-    v = umax64(v, dpp64<QE_DPP_MIRROR>(v));
-    unsigned al, bl, ah, bh;
-    rows16((unsigned)v, al, bl);
-    rows16((unsigned)(v >> 32), ah, bh);
-    v = umax64(((uint64_t)ah << 32) | al, ((uint64_t)bh << 32) | bl);
-    rows32((unsigned)v, al, bl);
-    rows32((unsigned)(v >> 32), ah, bh);
-    return umax64(((uint64_t)ah << 32) | al, ((uint64_t)bh << 32) | bl);
 }
 
 // ---------------------------------------------------------------------------
@@ -263,32 +241,6 @@ QE_DEV int wave_topk_vals(const float v_in[4], float lg_sh, int lane, int32_t *i
     if (lane == QE_K_USED) *shg = 1.f / (1.f + expf(-lg_sh));
     return myid;
 }
-QE_DEV void wave_topk(const float *lg, int lane, int32_t *ids, float *wts, float *shg) {
-    float v[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) v[j] = lg[lane + 64 * j];
-    wave_topk_vals(v, lg[QE_N_EXPERT], lane, ids, wts, shg);
-}
-
-// Exclusive scan of one int per thread over a 256-thread block; returns the
-// exclusive prefix, *total gets the sum.  `tmp` is 256 ints of LDS.
-QE_DEV int block_scan256(int v, int *tmp, int *total) {
-    const int tid = threadIdx.x;
-    tmp[tid] = v;
-    __syncthreads();
-#pragma unroll
-    for (int off = 1; off < 256; off <<= 1) {
-        const int a = tid >= off ? tmp[tid - off] : 0;
-        __syncthreads();
-        tmp[tid] += a;
-        __syncthreads();
-    }
-    const int incl = tmp[tid];
-    *total = tmp[255];
-    __syncthreads();
-    return incl - v;
-}
-
 // One canonical normalisation of a 2048-vector by one wave.  Lane c owns the
 // 32 contiguous elements [32c, 32c+32) in v[]; on return v holds xn.
 QE_DEV void wave_norm_chunk(float v[32], const float *post_norm, int lane) {
