@@ -153,7 +153,8 @@ int qe_moe_load_pack(qe_moe_ctx *ctx, const char *path, int pack_first, int firs
 #define QE_SRC_BF16 30
 
 /* `rows` rows of `cols` source weights -> NL4 rows of cols/2 code bytes then
- * cols/32 fp16 scales, contiguous in `dst`.  cols must be a multiple of 256,
+ * cols/32 fp16 scales, contiguous in `dst`, on the calling thread's current
+ * device (no context).  cols must be a multiple of 256,
  * src and dst 16-byte aligned, rows * cols / 32 < 2^31.  Replaces quant_row
  * (F_NL4) over dequant_rows' output (engine/qconv.cpp:91-98, :17-43). */
 int qe_moe_nl4_quantize_rows(const void *src, int src_type, int64_t rows, int cols, void *dst, void *stream);

@@ -129,7 +129,6 @@ int qe_moe_create(int device, int n_layers, int t_max, qe_moe_ctx **out) {
     A(S.sd, T * QE_D * 4);
     A(S.yp, NP * QE_D * 4);
     A(S.chunk_hist, nch * QE_N_EXPERT * 4);
-    A(S.counter, 256);
     A(c->bias_on, L);
     A(c->ex, (size_t)QE_DECODE_EX_WORDS * 8);
     A(c->sync, QE_DECODE_SYNC_WORDS * 4);
@@ -144,7 +143,7 @@ int qe_moe_create(int device, int n_layers, int t_max, qe_moe_ctx **out) {
     }
     S.t_max = t_max;
     S.prof = &c->prof;
-    if (hipMemset(S.counter, 0, 256) != hipSuccess || hipMemset(c->bias, 0, L * QE_N_EXPERT * 4) != hipSuccess ||
+    if (hipMemset(c->bias, 0, L * QE_N_EXPERT * 4) != hipSuccess ||
         hipMemset(c->bias_on, 0, L) != hipSuccess || hipMemset(c->sync, 0, QE_DECODE_SYNC_WORDS * 4) != hipSuccess ||
         hipMemset(c->err, 0, 256) != hipSuccess ||
         hipMemset(c->ex, 0, (size_t)QE_DECODE_EX_WORDS * 8) != hipSuccess ||

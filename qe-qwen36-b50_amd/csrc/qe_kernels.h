@@ -62,7 +62,6 @@ struct QeScratch {
     float *sd;                              // [T][2048] shared-expert output
     float *yp;                              // [T*8][2048] weighted expert outputs
     int32_t *chunk_hist;                    // [T*8/1024][256]
-    uint32_t *counter;                      // last-block ticket (self-resetting)
     int t_max;
     QeProf *prof;                           // host-side timing, may be nullptr
 };

@@ -653,7 +653,7 @@ __global__ __launch_bounds__(256) void k_router_shgu(const float *xn, const _Flo
     } sm;
     static_assert(RT_SPLIT % 8 == 0, "router groups divide evenly over the XCDs");
     const int x = blockIdx.x & 7, k = blockIdx.x >> 3;
-    const int mt64 = (T + 63) / 64, mt32 = (T + 31) / 32;
+    const int mt64 = (T + 63) / 64;
     const int nr = rs_router_per_xcd(T), ns = rs_shgu_per_xcd(T, x), both = 2 * (nr < ns ? nr : ns);
     bool router;
     int idx;
@@ -672,7 +672,6 @@ __global__ __launch_bounds__(256) void k_router_shgu(const float *xn, const _Flo
         if (idx >= ns) return;
         shgu_tile(xhl, T, Wg, hhl, 8 * (idx / RS_JT) + x, idx % RS_JT, sm.s);
     }
-    (void)mt32;
 }
 
 // From QE_RS_SPLIT_T tokens on, the two kinds run as two launches instead: the
