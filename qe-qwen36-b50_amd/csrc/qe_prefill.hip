@@ -441,8 +441,9 @@ __global__ __launch_bounds__(256, 2) void k_expert_gu(GemmTileArgs a) {
 // B operand is one 16-byte run of a Q8 row.
 //   gate/up: workgroup = 32 tokens x (gate rows j0..j0+31, up rows j0..j0+31),
 //            the four waves split K in quarters, partial sums meet in LDS,
-//            h = silu(g) * u is written as hi|lo halves.
-//   down:    workgroup = 32 tokens x 128 output rows, 32 per wave, full K.
+//            h = silu(g) * u is written as hi|lo halves (below 2048 tokens;
+//            from there shgu_tile64).
+//   down:    workgroup = 64 tokens x 128 output rows, LDS-staged (shdn_tile64).
 // Rows T..T+31 of the last tile exist in the buffers (sized for whole tiles) and
 // are never stored; each output row depends on its own A row only.
 // ===========================================================================
@@ -782,42 +783,80 @@ __global__ __launch_bounds__(256) void k_shgu(const _Float16 *xhl, int T, const 
     shgu_tile64(xhl, T, Wg, hhl, mp, k % 8, sm);
 }
 
-QE_DEV void shdn_tile(const _Float16 *hhl, int T, const uint8_t *W, float *out, int m_tile, int n_tile) {
+// Shared down, 64 tokens x 128 output rows per workgroup: wave w takes token
+// tile w & 1 and rows 64 (w >> 1) + 0..63 (two 32-row MFMA tiles) over the full
+// K = 512.  Per 32-block the workgroup stages 8 KB of h halves and 4 KB of Q8
+// rows in LDS once (double-buffered), so every fetched byte feeds two waves; the
+// 128 rows' block scales sit in LDS block-major for the whole K.  It runs in the
+// routed down kernel's LDS (28 KB of its 40).
+struct Shdn64Lds {
+    alignas(16) uint8_t a[2][2][4096];   // [stage][token tile][32-block of hi|lo halves]
+    alignas(16) uint8_t w[2][128][32];   // [stage][row][32 int8]
+    _Float16 sc[QE_FF_SH / 32][128];     // [block][row]
+};
+QE_DEV void shdn_tile64(const _Float16 *hhl, int T, const uint8_t *W, float *out, int mp, int n_tile, uint8_t *lds) {
     constexpr uint32_t RB = QE_SH_DN_ROW_BYTES;
     constexpr int NB = QE_FF_SH / 32;
+    Shdn64Lds &sm = *(Shdn64Lds *)lds;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, c = lane & 31, kh = lane >> 5;
-    const int m0 = m_tile * 32, n = n_tile * 128 + wv * 32 + c;
+    const int mt32 = (T + 31) / 32, n0 = n_tile * 128;
     const __amdgpu_buffer_rsrc_t ra =
-        __builtin_amdgcn_make_buffer_rsrc((void *)hhl, (short)0, ((T + 31) & ~31) * QE_FF_SH * 4, 0x00020000);
+        __builtin_amdgcn_make_buffer_rsrc((void *)hhl, (short)0, mt32 * 32 * QE_FF_SH * 4, 0x00020000);
     const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void *)W, (short)0, (int)QE_SH_DN_BYTES, 0x00020000);
-    const uint32_t a_off = (uint32_t)m_tile * NB * 4096 + lane * 16;
-    const uint32_t w_off = (uint32_t)n * RB;
-    qe_u32x4 sw[2];
+    {   // block scales: thread (row tid / 2, half tid & 1) brings 8 of the row's 16
+        const int r = tid >> 1, h = tid & 1;
+        const qe_u32x4 s = sh_ld(rw, (uint32_t)(n0 + r) * RB + QE_FF_SH + 16 * h);
 #pragma unroll
-    for (int i = 0; i < 2; ++i) sw[i] = sh_ld(rw, w_off + QE_FF_SH + 16 * i);
-    qe_float16v acc = {};
-    constexpr int DEPTH = 4;
-    qe_u32x4 ra_[DEPTH][4], rb[DEPTH];
-    auto load = [&](int b) {
-        const int s = b % DEPTH;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) ra_[s][q] = sh_ld(ra, a_off + 4096 * b + 1024 * q);
-        rb[s] = sh_ld(rw, w_off + 32 * b + 16 * kh);
-    };
-#pragma unroll
-    for (int b = 0; b < DEPTH; ++b) load(b);
-#pragma unroll
-    for (int b = 0; b < NB; ++b) {
-        const int s = b % DEPTH;
-        const qe_u32x4 a[4] = {ra_[s][0], ra_[s][1], ra_[s][2], ra_[s][3]};
-        const qe_u32x4 w = rb[s];
-        if (b + DEPTH < NB) load(b + DEPTH);
-        sh_block(a, w, half_of(sw, b), acc);
+        for (int e = 0; e < 8; ++e) {
+            const uint32_t v = s[e >> 1];
+            sm.sc[8 * h + e][r] = __builtin_bit_cast(_Float16, (uint16_t)((e & 1) ? v >> 16 : v & 0xffffu));
+        }
     }
+    uint32_t a_src[2];
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+        const int mt = 2 * mp + s < mt32 ? 2 * mp + s : mt32 - 1; // a tile past T reads the last one; never stored
+        a_src[s] = (uint32_t)mt * NB * 4096 + 16 * tid;
+    }
+    const int wr = tid >> 1, wh = tid & 1;
+    const uint32_t w_src = (uint32_t)(n0 + wr) * RB + 16 * wh;
+    qe_u32x4 st[3];
+    auto fetch = [&](int b) {
+        st[0] = sh_ld(ra, a_src[0] + 4096 * b);
+        st[1] = sh_ld(ra, a_src[1] + 4096 * b);
+        st[2] = sh_ld(rw, w_src + 32 * b);
+    };
+    auto put = [&](int s) {
+        *(qe_u32x4 *)&sm.a[s][0][16 * tid] = st[0];
+        *(qe_u32x4 *)&sm.a[s][1][16 * tid] = st[1];
+        *(qe_u32x4 *)&sm.w[s][wr][16 * wh] = st[2];
+    };
+    fetch(0);
+    put(0);
+    __syncthreads();
+    const int ms = wv & 1, r0 = 64 * (wv >> 1) + c, r1 = r0 + 32;
+    qe_float16v acc0 = {}, acc1 = {};
+#pragma unroll 2
+    for (int b = 0; b < NB; ++b) {
+        const int s = b & 1;
+        if (b + 1 < NB) fetch(b + 1);
+        qe_u32x4 av[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) av[q] = *(const qe_u32x4 *)&sm.a[s][ms][1024 * q + 16 * lane];
+        const qe_u32x4 w0 = *(const qe_u32x4 *)&sm.w[s][r0][16 * kh], w1 = *(const qe_u32x4 *)&sm.w[s][r1][16 * kh];
+        sh_block(av, w0, (float)sm.sc[b][r0], acc0);
+        sh_block(av, w1, (float)sm.sc[b][r1], acc1);
+        if (b + 1 < NB) put(s ^ 1); // stage s ^ 1 was last read in block b - 1, before the barrier
+        __syncthreads();
+    }
+    const int m0 = 64 * mp + 32 * ms;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
         const int m = m0 + 8 * (i >> 2) + 4 * kh + (i & 3);
-        if (m < T) out[(size_t)m * QE_D + n] = acc[i];
+        if (m < T) {
+            out[(size_t)m * QE_D + n0 + r0] = acc0[i];
+            out[(size_t)m * QE_D + n0 + r1] = acc1[i];
+        }
     }
 }
 
@@ -831,8 +870,13 @@ __global__ __launch_bounds__(256, 2) void k_expert_dn(GemmTileArgs a, int nr, co
     if (b < nr) {
         expert_unit<false>(a, b, sm);
     } else {
-        const int s = b - nr, mt = (T + 31) / 32;
-        shdn_tile(hhl, T, Wsd, sd, s % mt, s / mt);
+        const int s = b - nr;
+        // tile s runs on XCD s % 8 (nr is a multiple of 8 below): the 16 column
+        // tiles of one 64-token pair back to back there
+        const int x = s & 7, k = s >> 3, mp = 8 * (k / (QE_D / 128)) + x;
+        if (mp >= (T + 63) / 64) return;
+        static_assert(sizeof(Shdn64Lds) <= sizeof(sm.raw), "shared down staging fits the down tile's LDS");
+        shdn_tile64(hhl, T, Wsd, sd, mp, k % (QE_D / 128), sm.raw);
     }
 }
 
@@ -854,8 +898,8 @@ hipError_t qe_launch_expert_mfma(const QeLayerPtrs &L, const QeScratch &S, int T
     g.aq = S.xqp; g.a_bytes = T * QE_D; g.as = S.xs; g.a_row_div = QE_K_USED; g.hq = S.hqp; g.hs = S.hs;
     k_expert_gu<<<expert_max_wg<true>(np), 256, 0, st>>>(g);
     g.aq = S.hqp; g.a_bytes = np * QE_FF_EXP; g.as = S.hs; g.a_row_div = 1; g.yp = S.yp;
-    const int nsh = ((T + 31) / 32) * (QE_D / 128);
-    const int nr = expert_max_wg<false>(np);
+    const int nsh = 8 * (QE_D / 128) * (((T + 63) / 64 + 7) / 8);
+    const int nr = (expert_max_wg<false>(np) + 7) & ~7; // shared tiles start on XCD 0
     k_expert_dn<<<nr + nsh, 256, 0, st>>>(g, nr, (const _Float16 *)S.shgu, T, L.sh_dn, S.sd);
     return hipGetLastError();
 }
