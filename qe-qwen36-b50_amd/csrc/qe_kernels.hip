@@ -17,15 +17,40 @@
 // wave per token: xn, xq, xs
 __global__ __launch_bounds__(256) void k_normq(const float *x, int T, const float *post_norm, float *xn, int8_t *xqp,
                                                float *xs, _Float16 *xhl, int32_t *chunk_hist, int nch) {
-    const int lane = threadIdx.x & 63, t = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if ((int)blockIdx.x < nch) chunk_hist[blockIdx.x * QE_N_EXPERT + threadIdx.x] = 0; // dispatch histogram
-    if (t >= T) return;
-    float v[32];
-    load32(x + (size_t)t * QE_D + lane * 32, v);
-    wave_norm_chunk(v, post_norm, lane);
-    float4 *xo = (float4 *)(xn + (size_t)t * QE_D + lane * 32);
+    // the workgroup's four rows move through LDS: coalesced float4 loads and
+    // stores of the rows, lane c of wave w working on elements [32c, 32c+32) of
+    // row w (chunks padded to 33 words: conflict-free both ways)
+    __shared__ float s_r[4][64 * 33];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, t0 = blockIdx.x * 4, t = t0 + wv;
+    if ((int)blockIdx.x < nch) chunk_hist[blockIdx.x * QE_N_EXPERT + tid] = 0; // dispatch histogram
 #pragma unroll
-    for (int i = 0; i < 8; ++i) xo[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+    for (int i = 0; i < 8; ++i) { // row i / 2, float4 (i & 1) * 256 + tid
+        const int r = i >> 1, f = (i & 1) * 256 + tid, e = 4 * f;
+        if (t0 + r < T) {
+            const float4 q = ((const float4 *)(x + (size_t)(t0 + r) * QE_D))[f];
+            float *s = &s_r[r][(e >> 5) * 33 + (e & 31)];
+            s[0] = q.x; s[1] = q.y; s[2] = q.z; s[3] = q.w;
+        }
+    }
+    __syncthreads();
+    float v[32];
+    if (t < T) {
+#pragma unroll
+        for (int i = 0; i < 32; ++i) v[i] = s_r[wv][lane * 33 + i];
+        wave_norm_chunk(v, post_norm, lane);
+#pragma unroll
+        for (int i = 0; i < 32; ++i) s_r[wv][lane * 33 + i] = v[i];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int r = i >> 1, f = (i & 1) * 256 + tid, e = 4 * f;
+        if (t0 + r < T) {
+            const float *s = &s_r[r][(e >> 5) * 33 + (e & 31)];
+            ((float4 *)(xn + (size_t)(t0 + r) * QE_D))[f] = make_float4(s[0], s[1], s[2], s[3]);
+        }
+    }
+    if (t >= T) return;
     store_hilo_block(v, (uint8_t *)xhl, QE_D, t, lane);
     lane_quant_store_opnd(v, xqp + (size_t)t * QE_D, lane, xs + (size_t)t * (QE_D / 32) + lane);
 }
