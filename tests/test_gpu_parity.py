@@ -183,13 +183,14 @@ def test_cfg4_prefill_8192_skewed(ctx, torch_cuda):
     say(f"  distinct {np.count_nonzero(cnt)}, max/expert {cnt.max()}, <4 tokens {int(((cnt > 0) & (cnt < 4)).sum())}")
 
 
-@pytest.mark.parametrize("T,norm", [(33, False), (100, True), (257, False), (2085, True)])
+@pytest.mark.parametrize("T,norm", [(33, False), (100, True), (257, False), (2085, True), (4133, False)])
 def test_prefill_ragged_T(ctx, torch_cuda, T, norm):
     # T off the 32-token shared-expert tiles and the 64-token router tiles; the
     # context ran larger T before, so the padding rows of the last tiles hold
     # stale activations that must not leak into any output row.  2085 takes the
     # large-T launches (separate router and 64-token shared gate/up tiles) with a
-    # last token pair that has one 32-token tile past T
+    # last token pair that has one 32-token tile past T (4133: the same with 65
+    # token pairs)
     say(f"prefill T={T} (ragged tiles), norm+residual={norm}")
     x = O.gen_x(SEED, 300 + T, T)
     L, g = run_gpu(torch_cuda, ctx, 1, 1.0, x, norm=norm)
