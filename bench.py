@@ -178,7 +178,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
-              "multi-GPU expert sharding is design-only, see DESIGN.md", file=sys.stderr)
+              "multi-GPU expert sharding is design-only in this build", file=sys.stderr)
         sys.exit(2)
 
     import torch
