@@ -433,18 +433,35 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
         if (TM != 1 && wv == 0) {
             // stable counting sort of the T*8 pairs by expert (engine/qe.cpp:1965-1976):
             // slot of pair p = #pairs with a smaller expert + #earlier pairs with the same one
-            const int e = lane < np ? s_ids[lane] : 1 << 20;
-            int lt = 0, rank = 0, cnt = 0;
-            for (int q = 0; q < np; ++q) {
-                const int f = s_ids[q];
-                lt += f < e;
-                cnt += f == e;
-                rank += (f == e) & (q < lane);
+            // Counted by ballots over the 8 key bits, most significant first: at bit
+            // b, the lanes that share my key above b but hold 0 where I hold 1 are
+            // smaller; what remains after bit 0 are my peers.  (A loop over the
+            // pairs reading each key from LDS took ~4 us per layer at T = 8.)
+            const bool valid = lane < np;
+            const int e = valid ? s_ids[lane] : 1 << 20;
+            const unsigned long long below = (1ull << lane) - 1ull; // lane < 64
+            unsigned long long eq = __ballot(valid);
+            int lt = 0;
+#pragma unroll
+            for (int bit = 7; bit >= 0; --bit) {
+                const int my = (e >> bit) & 1;
+                const unsigned long long ones = __ballot(valid && my);
+                if (my) lt += __popcll(eq & ~ones);
+                eq &= my ? ones : ~ones;
             }
-            const bool first = lane < np && rank == 0;
+            const int rank = __popcll(eq & below), cnt = __popcll(eq);
+            const bool first = valid && rank == 0;
             const unsigned long long fm = __ballot(first);
+            // item = first-of-key lanes with a smaller key: the same walk over them
+            unsigned long long feq = fm;
             int item = 0;
-            for (int q = 0; q < np; ++q) item += (int)((fm >> q) & 1ull) & (s_ids[q] < e);
+#pragma unroll
+            for (int bit = 7; bit >= 0; --bit) {
+                const int my = (e >> bit) & 1;
+                const unsigned long long ones = __ballot(first && my);
+                if (my) item += __popcll(feq & ~ones);
+                feq &= my ? ones : ~ones;
+            }
             if (lane < np) s_pairs[lt + rank] = lane;
             if (first) s_items[item] = make_int4(e, lt, cnt, 0);
             if (lane == 0) s_misc[0] = __popcll(fm);
