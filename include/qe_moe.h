@@ -36,7 +36,8 @@ extern "C" {
 #define QE_ERR_ARG (-1)   /* bad argument (null pointer, layer or T out of range) */
 #define QE_ERR_HIP (-2)   /* a HIP runtime call failed */
 #define QE_ERR_OOM (-3)   /* device allocation failed */
-#define QE_ERR_STATE (-4) /* context not ready (weights of the layer never set) */
+#define QE_ERR_STATE (-4) /* layer not ready (a weight tensor or expert never set), or an earlier decode
+                              launch timed out in an exchange poll (see qe_moe_check) */
 
 typedef struct qe_moe_ctx qe_moe_ctx;
 
@@ -178,6 +179,24 @@ int qe_moe_arena_ptr(qe_moe_ctx *ctx, int layer, void **dev);
 int qe_moe_synth_layer(qe_moe_ctx *ctx, int layer, uint64_t seed, const float *bias, void *stream);
 /* Fill n fp32 activations N(0,1) of activation set `inst` on the device. */
 int qe_moe_synth_x(uint64_t seed, int inst, float *dev_out, int64_t n, void *stream);
+
+/* Decode poll timeouts.  The T <= 8 path synchronises workgroups through
+ * bounded polls; a poll that gives up (a hung or starved peer) lets the
+ * launch finish with invalid outputs and records it in a host-visible word.
+ * The next call that looks reports it once as QE_ERR_STATE and clears it:
+ * every forward entry point checks at entry (without synchronising, so a
+ * launch still running is reported by a later call), and qe_moe_get_routing,
+ * qe_moe_get_logits and qe_moe_check after synchronising `stream`.  The
+ * reference has no counterpart (its queue waits cannot fail). */
+int qe_moe_check(qe_moe_ctx *ctx, void *stream);
+
+/* Test hooks, no reference counterpart.  qe_moe_debug_set_epoch writes the
+ * decode launch counter (its low 16 bits tag the exchanged words), so a test
+ * can run launches across the counter's wrap; qe_moe_debug_set_spin_cap sets
+ * the reads an exchange poll makes before giving up (0 = the default), so a
+ * test can force a timeout without a stalled kernel. */
+int qe_moe_debug_set_epoch(qe_moe_ctx *ctx, uint32_t epoch, void *stream);
+int qe_moe_debug_set_spin_cap(qe_moe_ctx *ctx, int cap);
 
 const char *qe_moe_last_error(void);
 

@@ -41,13 +41,17 @@ struct qe_moe_ctx {
     uint8_t *sh_gu = nullptr;    // n_layers * SH_GU_BYTES
     uint8_t *sh_dn = nullptr;    // n_layers * SH_DN_BYTES
     float *post_norm = nullptr;  // n_layers * 2048
-    std::vector<uint8_t> has_bias, ready;
+    std::vector<uint8_t> has_bias;
+    std::vector<uint32_t> have;                  // per layer: HAVE_* bits of the tensors set so far
+    std::vector<std::vector<uint8_t>> have_exp;  // per layer: which of the 256 experts were supplied
     QeScratch S{};
     QeProf prof;
     uint8_t *bias_on = nullptr;  // device copy of has_bias
     uint64_t *ex = nullptr;      // decode exchange words
     unsigned *sync = nullptr;    // decode launch epoch + exit counter
-    unsigned *err = nullptr;     // decode barrier timeout flag
+    unsigned *err_host = nullptr; // pinned, host-mapped: 0, or 1 + epoch of a decode launch whose poll timed out
+    unsigned *err_dev = nullptr;  // the same word as the kernels address it
+    int spin_cap = QE_DECODE_SPIN_CAP;
     float *pingpong[2] = {nullptr, nullptr};
     std::vector<void *> allocs;
 };
@@ -67,6 +71,34 @@ static int dalloc(qe_moe_ctx *c, void **p, size_t bytes, bool zero = true) {
 static void free_all(qe_moe_ctx *c) {
     for (void *p : c->allocs) (void)hipFree(p);
     c->allocs.clear();
+    if (c->err_host) (void)hipHostFree(c->err_host);
+    c->err_host = nullptr;
+}
+
+// What a layer needs before a forward call may run on it.
+enum : uint32_t { HAVE_NORM = 1, HAVE_ROUTER = 2, HAVE_SH_GU = 4, HAVE_SH_DN = 8, HAVE_ALL_DENSE = 15 };
+static void mark_experts(qe_moe_ctx *c, int layer, int first, int n) {
+    for (int e = first; e < first + n; ++e) c->have_exp[layer][e] = 1;
+}
+static bool layer_ready(const qe_moe_ctx *c, int layer, std::string &missing) {
+    static const char *const names[4] = {"post_norm", "router", "sh_gu", "sh_down"};
+    missing.clear();
+    for (int b = 0; b < 4; ++b)
+        if (!(c->have[layer] & (1u << b))) missing += std::string(missing.empty() ? "" : ", ") + names[b];
+    int nexp = 0;
+    for (uint8_t h : c->have_exp[layer]) nexp += h;
+    if (nexp < QE_N_EXPERT)
+        missing += std::string(missing.empty() ? "" : ", ") + std::to_string(QE_N_EXPERT - nexp) + " experts";
+    return missing.empty();
+}
+
+// A decode launch whose exchange poll timed out leaves 1 + its epoch in the
+// host-mapped error word.  Reported once, by the next call that looks.
+static int take_decode_error(qe_moe_ctx *c, const char *where) {
+    const unsigned v = __atomic_exchange_n(c->err_host, 0u, __ATOMIC_ACQ_REL);
+    if (!v) return QE_OK;
+    return fail(QE_ERR_STATE, "%s: the decode launch of epoch %u timed out waiting for an exchange; its outputs are invalid",
+                where, v - 1u);
 }
 
 static QeLayerPtrs layer_ptrs(const qe_moe_ctx *c, int l) {
@@ -96,7 +128,8 @@ int qe_moe_create(int device, int n_layers, int t_max, qe_moe_ctx **out) {
     c->n_layers = n_layers;
     c->t_max = t_max;
     c->has_bias.assign(n_layers, 0);
-    c->ready.assign(n_layers, 0);
+    c->have.assign(n_layers, 0u);
+    c->have_exp.assign(n_layers, std::vector<uint8_t>(QE_N_EXPERT, 0));
     const size_t L = (size_t)n_layers, T = (size_t)t_max, NP = T * QE_K_USED, T32 = (T + 31) & ~(size_t)31;
     const size_t max_items = NP / (QE_MFMA_MC / 2 + 1) + 1 + QE_N_EXPERT; // big items hold > MC / 2 pairs
     const size_t nch = (NP + 1023) / 1024;
@@ -132,10 +165,25 @@ int qe_moe_create(int device, int n_layers, int t_max, qe_moe_ctx **out) {
     A(c->bias_on, L);
     A(c->ex, (size_t)QE_DECODE_EX_WORDS * 8);
     A(c->sync, QE_DECODE_SYNC_WORDS * 4);
-    A(c->err, 256);
     A(c->pingpong[0], T * QE_D * 4);
     A(c->pingpong[1], T * QE_D * 4);
 #undef A
+    if (rc != QE_OK) {
+        free_all(c);
+        delete c;
+        return rc;
+    }
+    if (rc == QE_OK) {
+        void *h = nullptr, *d = nullptr;
+        if (hipHostMalloc(&h, 256, hipHostMallocMapped | hipHostMallocCoherent) != hipSuccess)
+            rc = fail(QE_ERR_OOM, "hipHostMalloc of the error word failed");
+        else if ((c->err_host = (unsigned *)h), hipHostGetDevicePointer(&d, h, 0) != hipSuccess)
+            rc = fail(QE_ERR_HIP, "hipHostGetDevicePointer of the error word failed");
+        else {
+            c->err_dev = (unsigned *)d;
+            memset(h, 0, 256);
+        }
+    }
     if (rc != QE_OK) {
         free_all(c);
         delete c;
@@ -145,7 +193,6 @@ int qe_moe_create(int device, int n_layers, int t_max, qe_moe_ctx **out) {
     S.prof = &c->prof;
     if (hipMemset(c->bias, 0, L * QE_N_EXPERT * 4) != hipSuccess ||
         hipMemset(c->bias_on, 0, L) != hipSuccess || hipMemset(c->sync, 0, QE_DECODE_SYNC_WORDS * 4) != hipSuccess ||
-        hipMemset(c->err, 0, 256) != hipSuccess ||
         hipMemset(c->ex, 0, (size_t)QE_DECODE_EX_WORDS * 8) != hipSuccess ||
         hipDeviceSynchronize() != hipSuccess) {
         free_all(c);
@@ -175,6 +222,7 @@ int qe_moe_upload_experts(qe_moe_ctx *c, int layer, int first, int n, const void
     uint8_t *dst = c->arena + (size_t)layer * QE_LAYER_EXPERT_BYTES + (size_t)first * QE_EXPERT_BYTES;
     HIP_TRY(hipMemcpyAsync(dst, src, (size_t)n * QE_EXPERT_BYTES, on_dev ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice,
                            (hipStream_t)stream));
+    mark_experts(c, layer, first, n);
     return QE_OK;
 }
 
@@ -187,6 +235,8 @@ int qe_moe_set_dense(qe_moe_ctx *c, int layer, const float *post_norm, const flo
     const QeLayerPtrs L = layer_ptrs(c, layer);
     if (post_norm) HIP_TRY(hipMemcpyAsync((void *)L.post_norm, post_norm, QE_D * 4, k, s));
     if (router) HIP_TRY(hipMemcpyAsync((void *)L.router, router, QE_ROUTER_BYTES, k, s));
+    c->have[layer] |= (post_norm ? HAVE_NORM : 0u) | (router ? HAVE_ROUTER : 0u) | (sh_gu ? HAVE_SH_GU : 0u) |
+                      (sh_down ? HAVE_SH_DN : 0u);
     if (bias) {
         HIP_TRY(hipMemcpyAsync(c->bias + (size_t)layer * QE_N_EXPERT, bias, QE_N_EXPERT * 4, k, s));
         c->has_bias[layer] = 1;
@@ -195,7 +245,6 @@ int qe_moe_set_dense(qe_moe_ctx *c, int layer, const float *post_norm, const flo
     if (sh_gu) HIP_TRY(hipMemcpyAsync((void *)L.sh_gu, sh_gu, QE_SH_GU_BYTES, k, s));
     if (sh_down) HIP_TRY(hipMemcpyAsync((void *)L.sh_dn, sh_down, QE_SH_DN_BYTES, k, s));
     if (!on_dev) HIP_TRY(hipStreamSynchronize(s)); /* host sources need not outlive the call */
-    c->ready[layer] = 1;
     return QE_OK;
 }
 
@@ -301,7 +350,8 @@ int qe_moe_load_pack(qe_moe_ctx *c, const char *path, int pack_first, int first_
         c->has_bias[l] = 0;
         HIP_TRY(hipMemcpyAsync(c->bias_on + l, &c->has_bias[l], 1, hipMemcpyHostToDevice, s));
         HIP_TRY(hipStreamSynchronize(s)); // the mapping goes away with this call
-        c->ready[l] = 1;
+        c->have[l] = HAVE_ALL_DENSE;
+        mark_experts(c, l, 0, QE_N_EXPERT);
     }
     return QE_OK;
 }
@@ -310,9 +360,10 @@ static int check_fwd(qe_moe_ctx *c, int layer, const void *in, const void *out, 
     if (!c || !in || !out || T <= 0) return fail(QE_ERR_ARG, "forward: bad argument");
     if (layer < 0 || layer >= c->n_layers) return fail(QE_ERR_ARG, "forward: layer %d out of range", layer);
     if (T > c->t_max) return fail(QE_ERR_ARG, "forward: T=%d exceeds t_max=%d", T, c->t_max);
-    if (!c->ready[layer]) return fail(QE_ERR_STATE, "forward: layer %d has no dense weights", layer);
+    std::string missing;
+    if (!layer_ready(c, layer, missing)) return fail(QE_ERR_STATE, "forward: layer %d lacks %s", layer, missing.c_str());
     if (in == out) return fail(QE_ERR_ARG, "forward: output may not alias the input");
-    return QE_OK;
+    return take_decode_error(c, "forward");
 }
 
 // T <= QE_SMALL_T: every layer of the range in one persistent launch.
@@ -326,7 +377,7 @@ static hipError_t run_decode(qe_moe_ctx *c, int first, int n, const float *in, f
     d.ex = c->ex;
     d.logits = c->S.logits; d.ids = c->S.ids; d.wts = c->S.wts; d.shg = c->S.shg; d.off = c->S.off; d.pairs = c->S.pairs;
     d.sd_out = c->S.sd; d.xn_out = c->S.xn;
-    d.sync = c->sync; d.err = c->err;
+    d.sync = c->sync; d.err = c->err_dev; d.spin_cap = c->spin_cap;
     d.exit_norm = exit_norm; d.exit_xn = exit_xn;
     ProfScope ps(&c->prof, QP_DECODE, st);
     return qe_launch_decode(d, st);
@@ -399,11 +450,8 @@ int qe_moe_get_routing(qe_moe_ctx *c, int T, int32_t *ids, float *wts, float *sh
     if (off) HIP_TRY(hipMemcpyAsync(off, c->S.off, (QE_N_EXPERT + 1) * 4, hipMemcpyDeviceToHost, s));
     if (pairs) HIP_TRY(hipMemcpyAsync(pairs, c->S.pairs, np * 4, hipMemcpyDeviceToHost, s));
     if (shared_out) HIP_TRY(hipMemcpyAsync(shared_out, c->S.sd, (size_t)T * QE_D * 4, hipMemcpyDeviceToHost, s));
-    unsigned err = 0;
-    HIP_TRY(hipMemcpyAsync(&err, c->err, 4, hipMemcpyDeviceToHost, s));
     HIP_TRY(hipStreamSynchronize(s));
-    if (err) return fail(QE_ERR_STATE, "get_routing: a decode exchange poll timed out (results invalid)");
-    return QE_OK;
+    return take_decode_error(c, "get_routing");
 }
 
 int qe_moe_dispatch(qe_moe_ctx *c, const int32_t *ids, int T, void *stream) {
@@ -419,6 +467,29 @@ int qe_moe_get_logits(qe_moe_ctx *c, int T, float *logits, void *stream) {
     HIP_TRY(hipSetDevice(c->device));
     HIP_TRY(hipMemcpyAsync(logits, c->S.logits, (size_t)T * QE_ROUTER_ROWS * 4, hipMemcpyDeviceToHost, (hipStream_t)stream));
     HIP_TRY(hipStreamSynchronize((hipStream_t)stream));
+    return take_decode_error(c, "get_logits");
+}
+
+int qe_moe_check(qe_moe_ctx *c, void *stream) {
+    if (!c) return fail(QE_ERR_ARG, "check: bad argument");
+    HIP_TRY(hipSetDevice(c->device));
+    HIP_TRY(hipStreamSynchronize((hipStream_t)stream));
+    return take_decode_error(c, "check");
+}
+
+int qe_moe_debug_set_epoch(qe_moe_ctx *c, uint32_t epoch, void *stream) {
+    if (!c) return fail(QE_ERR_ARG, "debug_set_epoch: bad argument");
+    HIP_TRY(hipSetDevice(c->device));
+    static uint32_t v;  // a pageable source is copied before hipMemcpyAsync returns
+    v = epoch;
+    HIP_TRY(hipMemcpyAsync(c->sync, &v, 4, hipMemcpyHostToDevice, (hipStream_t)stream));
+    HIP_TRY(hipStreamSynchronize((hipStream_t)stream));
+    return QE_OK;
+}
+
+int qe_moe_debug_set_spin_cap(qe_moe_ctx *c, int cap) {
+    if (!c || cap < 0) return fail(QE_ERR_ARG, "debug_set_spin_cap: bad argument");
+    c->spin_cap = cap > 0 ? cap : QE_DECODE_SPIN_CAP;
     return QE_OK;
 }
 
@@ -520,12 +591,14 @@ int qe_moe_convert_experts(qe_moe_ctx *c, int layer, const void *gate, const voi
     a.src = (const uint8_t *)down;
     a.dst = base + QE_EXPERT_DOWN_OFF;
     HIP_TRY(qe_launch_nl4_quant(a, src_type, (hipStream_t)stream));
+    mark_experts(c, layer, 0, QE_N_EXPERT);
     return QE_OK;
 }
 
 int qe_moe_arena_ptr(qe_moe_ctx *c, int layer, void **dev) {
     if (!c || !dev || layer < 0 || layer >= c->n_layers) return fail(QE_ERR_ARG, "arena_ptr: bad argument");
     *dev = c->arena + (size_t)layer * QE_LAYER_EXPERT_BYTES;
+    mark_experts(c, layer, 0, QE_N_EXPERT); // the caller fills the arena in place
     return QE_OK;
 }
 
@@ -544,7 +617,8 @@ int qe_moe_synth_layer(qe_moe_ctx *c, int layer, uint64_t seed, const float *bia
     }
     HIP_TRY(hipMemcpyAsync(c->bias_on + layer, &c->has_bias[layer], 1, hipMemcpyHostToDevice, (hipStream_t)stream));
     HIP_TRY(hipStreamSynchronize((hipStream_t)stream));
-    c->ready[layer] = 1;
+    c->have[layer] = HAVE_ALL_DENSE;
+    mark_experts(c, layer, 0, QE_N_EXPERT);
     return QE_OK;
 }
 

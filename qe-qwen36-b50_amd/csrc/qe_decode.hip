@@ -45,7 +45,6 @@
 #define SYNC_EPOCH 0
 #define SYNC_EXIT 32
 #define REP QE_DEC_REP      /* copies of every exchanged buffer and counter */
-#define SPIN_CAP (1 << 22)
 #define DEC_MIN_GRID 64   /* D row groups per workgroup stay <= 4 */
 #define N_RTASK (QE_ROUTER_ROWS + QE_FF_SH) /* router rows, then shared (gate, up) row pairs */
 
@@ -93,13 +92,26 @@ static_assert(SYNC_EXIT < QE_DECODE_SYNC_WORDS, "sync words must match the alloc
 QE_DEV uint64_t pack_tv(float v, unsigned tag) { return ((uint64_t)tag << 32) | __float_as_uint(v); }
 QE_DEV float tv_val(uint64_t w) { return __uint_as_float((unsigned)w); }
 
+// Bounded polling: after pc.cap failed reads a poll gives up, records the
+// launch in the host-visible error word (system scope: the host reads it
+// without synchronising the stream) and goes on with what it read, so every
+// wave still reaches the end of the kernel.
+struct PollCtl {
+    unsigned *err;  // host-mapped word: 0, or 1 + the epoch of a launch whose poll timed out
+    int cap;        // reads a poll makes before it gives up
+    unsigned val;   // what this launch records
+};
+QE_DEV void poll_timeout(const PollCtl &pc) {
+    __hip_atomic_store(pc.err, pc.val, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
 // Read N tagged words w[i] = src[i * stride] until every one carries `tag`
-// (wave-uniform retry, bounded; a timeout sets *err).  Inactive lanes read nothing.
+// (wave-uniform retry, at most pc.cap reads).  Inactive lanes read nothing.
 // One read in flight per retry: measured against two, four and six staggered
 // reads per poller, the extra polling traffic delayed the producers' stores
 // more than it shortened detection (1,680 vs 1,620 / 1,551 / 1,494 tokens/s).
 template <int N>
-QE_DEV void read_tv(const uint64_t *src, int stride, unsigned tag, uint64_t w[N], bool act, unsigned *err) {
+QE_DEV void read_tv(const uint64_t *src, int stride, unsigned tag, uint64_t w[N], bool act, const PollCtl &pc) {
     for (int spins = 0;; ++spins) {
         unsigned bad = 0;
 #pragma unroll
@@ -108,7 +120,7 @@ QE_DEV void read_tv(const uint64_t *src, int stride, unsigned tag, uint64_t w[N]
             bad |= (unsigned)(w[i] >> 32) ^ tag;
         }
         if (__all(bad == 0)) break;
-        if (spins > SPIN_CAP) { ST_A(err, 1u); break; }
+        if (spins + 1 >= pc.cap) { poll_timeout(pc); break; }
         __builtin_amdgcn_s_sleep(1);
     }
 }
@@ -182,6 +194,7 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
     if (threadIdx.x == 0) s_misc[1] = (int)LD_A(a.sync + SYNC_EPOCH);
     __syncthreads();
     const unsigned epoch = (unsigned)s_misc[1];
+    const PollCtl pc{a.err, a.spin_cap, 1u + (epoch & 0x7fffffffu)};
     uint64_t *EX = a.ex;                                   // replica 0 (writes go to all REP)
     const uint64_t *EXr = a.ex + (size_t)(blockIdx.x % REP) * EX_TOTAL; // the copy this workgroup reads
     constexpr bool mode16 = TM == 1; // 16-row units, fp32 h (one token: 8 items x 32 units fill the grid)
@@ -251,7 +264,7 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
         }
         if (li > 0 && tid < T * 256) { // x: one word per (8-row group, token) polled first; the
             uint64_t w[1];               // rest of the workgroup polls its own words directly
-            read_tv<1>(src_x + (tid >> 8) * QE_D + (tid & 255) * 8 + 7, 0, tagIn, w, true, a.err);
+            read_tv<1>(src_x + (tid >> 8) * QE_D + (tid & 255) * 8 + 7, 0, tagIn, w, true, pc);
         }
         // raw x of all tokens -> LDS (natural layout, token stride 2048; T*2048 is a multiple of 2 NTH)
         if (li == 0) {
@@ -259,7 +272,7 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
         } else {
             for (int i0 = 0; i0 < T * QE_D; i0 += 2 * NTH) {
                 uint64_t w[2];
-                read_tv<2>(src_x + i0 + tid, NTH, tagIn, w, true, a.err);
+                read_tv<2>(src_x + i0 + tid, NTH, tagIn, w, true, pc);
                 const int e0 = i0 + tid, e1 = e0 + NTH;
                 s_xn[(e0 >> 11) * DEC_XSTR + xpos(e0 & 2047)] = tv_val(w[0]);
                 s_xn[(e1 >> 11) * DEC_XSTR + xpos(e1 & 2047)] = tv_val(w[1]);
@@ -384,8 +397,8 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
         if (wv < T) {
             const int t = wv;
             uint64_t w[5];
-            read_tv<4>(EXr + EX_L + t * QE_ROUTER_ROWS + lane, 64, tagR, w, true, a.err);
-            read_tv<1>(EXr + EX_L + t * QE_ROUTER_ROWS + QE_N_EXPERT, 0, tagR, w + 4, true, a.err);
+            read_tv<4>(EXr + EX_L + t * QE_ROUTER_ROWS + lane, 64, tagR, w, true, pc);
+            read_tv<1>(EXr + EX_L + t * QE_ROUTER_ROWS + QE_N_EXPERT, 0, tagR, w + 4, true, pc);
             float v[5];
 #pragma unroll
             for (int j = 0; j < 5; ++j) v[j] = tv_val(w[j]);
@@ -399,11 +412,13 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
                 // one token: its 8 distinct experts are the items, in expert order
                 // (engine/qe.cpp:1965-1976 with one pair per expert): lane k < 8
                 // holds pair k's expert, and its slot is the count of smaller ids
+                // (plus equal ids of earlier pairs, so the slots stay a permutation
+                // of 0..7 even if a timed-out poll fed the top-8 garbage)
                 int id8[QE_K_USED], rank = 0;
 #pragma unroll
                 for (int j = 0; j < QE_K_USED; ++j) {
                     id8[j] = __builtin_amdgcn_readlane(myid, j);
-                    rank += id8[j] < myid;
+                    rank += id8[j] < myid || (id8[j] == myid && j < lane);
                 }
                 if (lane < QE_K_USED) {
                     s_pairs[rank] = lane;
@@ -574,7 +589,7 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
         // shared-expert activations of every token: written in R, long landed by now
         for (int i = tid; i < T * QE_FF_SH; i += NTH) {
             uint64_t w[1];
-            read_tv<1>(EXr + EX_HSH + i, 0, tagR, w, true, a.err);
+            read_tv<1>(EXr + EX_HSH + i, 0, tagR, w, true, pc);
             s_hsh[i] = tv_val(w[0]);
         }
         __syncthreads();
@@ -608,13 +623,13 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
         }
         if (mode16 && tid < 256) {
             uint64_t w[1];
-            read_tv<1>(EXr + EX_HF + (tid >> 5) * QE_FF_EXP + (tid & 31) * 16 + 15, 0, tagG, w, true, a.err);
+            read_tv<1>(EXr + EX_HF + (tid >> 5) * QE_FF_EXP + (tid & 31) * 16 + 15, 0, tagG, w, true, pc);
         }
         if (mode16) { // fp32 h of the 8 pairs -> LDS, then int8 per 32 rows
             // thread = 4 consecutive h of one pair, 8 lanes per 32-block (quant_x per block)
             static_assert(8 * QE_FF_EXP == 4 * NTH, "h of the 8 pairs: four words per thread");
             uint64_t w[4];
-            read_tv<4>(EXr + EX_HF + 4 * tid, 1, tagG, w, true, a.err);
+            read_tv<4>(EXr + EX_HF + 4 * tid, 1, tagG, w, true, pc);
             float h[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) h[i] = tv_val(w[i]);
@@ -633,7 +648,7 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
             for (int task = tid; task < np * 16; task += NTH) { // (pair, 32-block): 8 code words + 1 scale
                 const int p = task >> 4, b = task & 15;
                 uint64_t w[9];
-                read_tv<9>(EXr + EX_HQ + ((size_t)p * 16 + b) * 9, 1, tagG, w, true, a.err);
+                read_tv<9>(EXr + EX_HQ + ((size_t)p * 16 + b) * 9, 1, tagG, w, true, pc);
                 uint4 *dq = (uint4 *)(s_hq + p * QE_FF_EXP + b * 32);
                 dq[0] = make_uint4((unsigned)w[0], (unsigned)w[1], (unsigned)w[2], (unsigned)w[3]);
                 dq[1] = make_uint4((unsigned)w[4], (unsigned)w[5], (unsigned)w[6], (unsigned)w[7]);
@@ -716,7 +731,7 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
         const uint64_t *src = EXr + EX_X + (size_t)(li & 1) * DEC_T * QE_D + (size_t)t * QE_D;
         for (int i = threadIdx.x; i < QE_D; i += NTH) {
             uint64_t w[1];
-            read_tv<1>(src + i, 0, tagX, w, true, a.err);
+            read_tv<1>(src + i, 0, tagX, w, true, pc);
             s_xn[xpos(i)] = tv_val(w[0]);
         }
         __syncthreads();
@@ -736,12 +751,29 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
             a.exit_xn[(size_t)t * QE_D + e] = (s_xn[xpos(e)] * s_inv[0]) * a.exit_norm[e];
     }
 
-    // the last workgroup out advances the epoch, so the next launch uses new tags
+    // The last workgroup out advances the epoch, so the next launch uses new
+    // tags.  Tags carry the epoch modulo 65536: a word that no launch rewrote
+    // for exactly k * 65536 launches (EX_HF is written only by T = 1 launches,
+    // EX_HQ only by T > 1, the slots of tokens >= T by larger batches) would
+    // match a poll before its producer stores it.  So when the low 16 bits of
+    // the epoch are about to wrap, the last workgroup out (every other one has
+    // finished reading) zeroes the exchange: tag 0 is never expected (stage
+    // numbers start at 1), and every word written after the wrap carries an
+    // epoch that no earlier word of the same 65536-launch window holds.
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    if (threadIdx.x == 0 && ADD_A(a.sync + SYNC_EXIT, 1u) == gridDim.x - 1) {
-        ST_A(a.sync + SYNC_EXIT, 0u);
-        ST_A(a.sync + SYNC_EPOCH, epoch + 1u);
+    if (threadIdx.x == 0) s_misc[2] = ADD_A(a.sync + SYNC_EXIT, 1u) == gridDim.x - 1;
+    __syncthreads();
+    if (s_misc[2]) {
+        if (((epoch + 1u) & 0xffffu) == 0u) {
+            for (size_t i = threadIdx.x; i < (size_t)QE_DECODE_EX_WORDS; i += NTH) ST_A(a.ex + i, (uint64_t)0);
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+        }
+        if (threadIdx.x == 0) {
+            ST_A(a.sync + SYNC_EXIT, 0u);
+            ST_A(a.sync + SYNC_EPOCH, epoch + 1u);
+        }
     }
 }
 

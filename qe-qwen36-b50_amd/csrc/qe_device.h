@@ -220,7 +220,7 @@ QE_DEV int wave_topk_vals(const float v_in[4], float lg_sh, int lane, int32_t *i
         for (int j = 3; j >= 0; --j) ck = v[j] == m ? key0 + 4 * j : ck;
         const unsigned kmin = wave_min_u32(ck);
         sel[k] = ord2f(m);
-        id[k] = (int)((kmin & 15) * 16 + (kmin >> 4));
+        id[k] = (int)(((kmin & 15u) << 4) | ((kmin >> 4) & 15u)); // in 0..255 whatever the data
 #pragma unroll
         for (int j = 0; j < 4; ++j)
             if (key0 + 4 * j == kmin) v[j] = 0u; // below every ordered float

@@ -84,7 +84,8 @@ struct QeDecodeArgs {
     // routing sink of the last layer (plain stores by workgroup 0)
     float *logits; int32_t *ids; float *wts; float *shg; int32_t *off; int32_t *pairs; float *sd_out; float *xn_out;
     unsigned *sync;      // QE_DECODE_SYNC_WORDS: [0] launch epoch, [32] exit counter
-    unsigned *err;       // set to 1 if a poll timed out
+    unsigned *err;       // host-mapped: set to 1 + epoch when a poll of the launch timed out
+    int spin_cap;        // reads an exchange poll makes before it gives up (QE_DECODE_SPIN_CAP)
     const float *exit_norm; float *exit_xn; // optional: exit_xn = RMSNorm(x_out) * exit_norm
 };
 hipError_t qe_launch_decode(const QeDecodeArgs &a, hipStream_t st);
@@ -94,6 +95,7 @@ hipError_t qe_launch_decode(const QeDecodeArgs &a, hipStream_t st);
 #define QE_DECODE_EX_WORDS \
     (QE_DEC_REP * (2 * QE_SMALL_T * QE_D + QE_SMALL_T * QE_ROUTER_ROWS + QE_SMALL_T * QE_FF_SH + QE_SMALL_T * 8 * 16 * 9 + 8 * QE_FF_EXP))
 #define QE_DECODE_SYNC_WORDS 64 /* launch epoch, exit counter */
+#define QE_DECODE_SPIN_CAP (1 << 22) /* poll reads (s_sleep 1 between) before an exchange wait gives up */
 
 // Launchers (qe_kernels.hip).  xin: layer input; post_norm: nullptr = input is
 // already normalised; x2: residual added to the output or nullptr.

@@ -331,7 +331,8 @@ hipError_t qe_launch_layer(const QeLayerPtrs &L, const QeScratch &S, const float
     }
     {
         QE_PROF(QP_ROUTER);
-        (void)qe_launch_router_shgu(L, S, T, st);
+        const hipError_t e = qe_launch_router_shgu(L, S, T, st);
+        if (e != hipSuccess) return e;
     }
     {
         QE_PROF(QP_TOPK);
@@ -346,7 +347,8 @@ hipError_t qe_launch_layer(const QeLayerPtrs &L, const QeScratch &S, const float
     }
     {
         QE_PROF(QP_GU); // routed gate/up, then routed down + shared down
-        (void)qe_launch_expert_mfma(L, S, T, st);
+        const hipError_t e = qe_launch_expert_mfma(L, S, T, st);
+        if (e != hipSuccess) return e;
     }
     {
         QE_PROF(QP_COMBINE);

@@ -88,6 +88,9 @@ def load(path: str = LIB_PATH):
         "qe_moe_profile_name": (ctypes.c_char_p, [i32]),
         "qe_moe_nl4_quantize_rows": (i32, [vp, i32, i64, i32, vp, vp]),
         "qe_moe_convert_experts": (i32, [vp, i32, vp, vp, vp, i32, vp]),
+        "qe_moe_check": (i32, [vp, vp]),
+        "qe_moe_debug_set_epoch": (i32, [vp, ctypes.c_uint32, vp]),
+        "qe_moe_debug_set_spin_cap": (i32, [vp, i32]),
     }
     for name, (res, args) in sig.items():
         f = getattr(lib, name)
@@ -195,6 +198,16 @@ class MoE:
         _check(_lib.qe_moe_get_routing(self.h, T, _ptr(ids), _ptr(wts), _ptr(shg), _ptr(off), _ptr(pairs), _ptr(sd),
                                        _stream(stream)))
         return dict(ids=ids, wts=wts, shg=shg, off=off, pairs=pairs, sd=sd)
+
+    def check(self, stream=None):
+        """Synchronise `stream`; raise QeError if a decode launch timed out in an exchange poll."""
+        _check(_lib.qe_moe_check(self.h, _stream(stream)))
+
+    def debug_set_epoch(self, epoch, stream=None):
+        _check(_lib.qe_moe_debug_set_epoch(self.h, epoch, _stream(stream)))
+
+    def debug_set_spin_cap(self, cap):
+        _check(_lib.qe_moe_debug_set_spin_cap(self.h, cap))
 
     def dispatch(self, ids_dev, T, stream=None):
         _check(_lib.qe_moe_dispatch(self.h, _ptr(ids_dev), T, _stream(stream)))

@@ -260,6 +260,83 @@ def test_full_layer_against_float64_restatement():
     assert np.linalg.norm(r["sd"][0] - sd) / np.linalg.norm(sd) < 1e-6
 
 
+def _router_f64(xn, W, bias):
+    """float64 logits of engine/qe.cpp:144-150 with the shared-gate row appended
+    as row 256 (:1055): W[e] . xn for e = 0..256, bias on rows 0..255 only; and
+    the sum of |terms|, which bounds any fp32 summation order's error."""
+    xd, Wd = xn.astype(np.float64), W.astype(np.float64)
+    lg, scale = xd @ Wd.T, np.abs(xd) @ np.abs(Wd).T
+    if bias is not None:
+        lg[:, :256] += bias.astype(np.float64)
+        scale[:, :256] += np.abs(bias.astype(np.float64))
+    return lg, scale
+
+
+def _router_matches(lg32, xn, W, bias):
+    ref, scale = _router_f64(xn, W, bias)
+    return lg32.shape == ref.shape and bool(np.all(np.abs(lg32.astype(np.float64) - ref) <= 1e-5 * scale))
+
+
+def test_router_against_float64():
+    L = O.SynthLayer(SEED, 3)
+    xn = O.rmsnorm(3.0 * O.gen_x(SEED, 21, 5), None)
+    bias = (0.5 + np.random.default_rng(21).random(256)).astype(np.float32)  # no entry near 0
+    for b in (None, bias):
+        assert _router_matches(O.router(xn, L.router, b), xn, L.router, b)
+    lg = O.router(xn, L.router, bias)
+    # row 256 is a plain dot with the shared-gate vector, no bias
+    g64 = xn.astype(np.float64) @ L.router[256].astype(np.float64)
+    assert np.all(np.abs(lg[:, 256] - g64) <= 1e-5 * (np.abs(xn) @ np.abs(L.router[256]).astype(np.float64)))
+    # planted slips fail the same check: bias also on row 256 (a loop to e <= 256
+    # reading bias[e % 256]), bias dropped, rows off by one, bias on the wrong row
+    bad = lg.copy()
+    bad[:, 256] += bias[0]
+    assert not _router_matches(bad, xn, L.router, bias)
+    assert not _router_matches(O.router(xn, L.router, None), xn, L.router, bias)
+    assert not _router_matches(O.router(xn, np.ascontiguousarray(np.roll(L.router, -1, 0)), bias), xn, L.router, bias)
+    assert not _router_matches(O.router(xn, L.router, np.ascontiguousarray(np.roll(bias, 1))), xn, L.router, bias)
+
+
+def _rel(a, b):
+    return float(np.linalg.norm(np.asarray(a, np.float64) - b) / np.linalg.norm(b))
+
+
+def test_layer_wiring_norm_and_residual_against_float64():
+    """moe_layer(norm, residual) is x + MoE(RMSNorm(x) * post_norm)
+    (engine/qe.cpp:1958 entry norm, :2036-2044 combine onto the residual), with
+    the norm, routing, weights and gate recomputed in float64 here."""
+    L = O.SynthLayer(SEED, 4)
+    # The MoE output does not depend on the input's scale (the norm removes it) and
+    # is ~3e4 in rms with these synthetic weights; x at rms 1e4 keeps the residual
+    # (and a skipped norm) visible at the 1e-4 bar.
+    x = (1e4 * O.gen_x(SEED, 22, 2)).astype(np.float32)
+    pn = (1.0 + 0.25 * O.gen_x(SEED, 23, 1)[0]).astype(np.float32)
+    r = O.moe_layer(L, x, norm=True, residual=True, post_norm=pn)
+    xd = x.astype(np.float64)
+    xn64 = xd / np.sqrt((xd ** 2).mean(axis=1, keepdims=True) + 1e-6) * pn.astype(np.float64)
+    assert _rel(r["xn"], xn64) < 1e-6
+    lg64, _ = _router_f64(xn64, L.router, None)
+    ids64 = np.stack([_topk_ref(lg64[t]) for t in range(2)])
+    assert np.array_equal(r["ids"], ids64)
+    sel = np.take_along_axis(lg64[:, :256], ids64, axis=1)
+    p = np.exp(sel - sel[:, :1])
+    wts64 = p / p.sum(axis=1, keepdims=True)
+    shg64 = 1.0 / (1.0 + np.exp(-lg64[:, 256]))
+    moe64 = _f64_layer(L, xn64.astype(np.float32), ids64, wts64, shg64)
+    ref = xd + moe64
+
+    def ok(out):
+        return _rel(out, ref) < 1e-4
+
+    assert ok(r["out"])
+    # planted wiring slips, each must fail: residual taken from the normed input,
+    # no residual, the norm skipped, the norm weight dropped
+    assert not ok(xn64 + moe64)
+    assert not ok(r["out"] - xd)
+    assert not ok(xd + O.moe_layer(L, x)["out"])
+    assert not ok(xd + O.moe_layer(L, O.rmsnorm(x, None))["out"])
+
+
 def test_scalar_and_avx2_layers_agree_bitwise():
     L = O.SynthLayer(SEED, 1, bias=O.gen_zipf_bias(SEED, 1, 1.0))
     x = O.gen_x(SEED, 2, 3)
