@@ -11,17 +11,23 @@ HBM arena, inputs resident in HBM before timing.  Also reported:
     peak vs the fp16 MFMA peak) and the routed grouped-GEMM rate alone;
   * prefill8192_zipf13: BASELINE config 4 (8192 tokens, one layer, Zipf s=1.3),
     472.5 GFLOP per call / time;
-  * decode_b8: 8 tokens per step through the 40-layer stack;
+  * cfg0_decode_b1_layer: BASELINE config 0, one layer, B=1, calls rotated
+    over the 40 resident layers (so the 256 MB MALL holds none of them);
+  * cfg1_decode_b8_zipf_layer: BASELINE config 1, one layer, B=8 with the
+    Zipf s=1 router bias, rotated over the 40 layers; bytes count each distinct
+    expert of a call once (the reference's accounting);
+  * stack40_b8: 8 tokens per step through the 40-layer stack (no bias);
   * convert_layer_q8_0: the IQ4_NL converter, one layer's routed experts
     (blk.N.ffn_{gate,up,down}_exps in Q8_0, the reference converter's input)
     quantized into the arena, against the CPU restatement of ggml's quantizer
     on a few experts (--convert-only runs just this, for profiling);
-  * roofline: the decode kernel (k_decode, the only kernel of a decode step)
-    timed with the library's HIP events on the launch stream over a profiled
-    pass of the same workload;
+  * roofline: the decode kernel (k_decode, the only kernel of a decode step:
+    one launch per step), its duration the timed region's HIP-event time per
+    step on the launch stream;
   * cpu_baseline: the CPU AVX2 restatement of the reference CPU MoE path
     (oracle/qe_oracle.cpp) on a bounded sample, host cores, same process, at
-    the box's thread share and at the reference's default of 12 threads.
+    the box's thread share and at the reference's default of 12 threads; the
+    prefill lines carry their own CPU baseline (GFLOP/s of the same layer).
 Weights are random-init from the seeded generator (no checkpoints offline).
 """
 import argparse
@@ -63,6 +69,46 @@ def timed(torch, fn, steps, stream):
     b.record(stream)
     torch.cuda.synchronize()
     return a.elapsed_time(b) / steps
+
+
+def layer_rotation(torch, m, x, y, T, n_layers, steps):
+    """One-layer calls (forward_normed: no norm, no residual) cycling over
+    n_layers resident layers, HIP events on the launch stream; ms per call."""
+    st = torch.cuda.current_stream()
+    i = [0]
+
+    def call():
+        m.forward_normed(i[0] % n_layers, x, y, T, stream=st)
+        i[0] += 1
+
+    for _ in range(n_layers):
+        call()
+    return timed(torch, call, steps, st)
+
+
+def cpu_prefill(T, inst, bias_s, threads, budget_s):
+    """The reference's batched CPU expert path (engine/qe.cpp:2050-2101, restated
+    in oracle/qe_oracle.cpp as orc_baseline_layer) over one whole prefill layer:
+    router, top-8, dispatch, int8 experts, Q8 shared expert, combine; the same
+    seeded layer (all 256 experts) and input as the GPU line.  Runs until
+    budget_s of timed work (at least once).  Returns (GFLOP/s, ms per call, calls)."""
+    sys.path.insert(0, os.path.join(REPO, "oracle"))
+    import oracle as O
+
+    import qe_moe
+
+    L = O.SynthLayer(SEED, 0, bias=qe_moe.synth_zipf_bias(SEED, 0, bias_s))
+    blobs = [O.gen_expert(SEED, 0, e) for e in range(256)]
+    ptrs = (ctypes.c_void_p * 256)()
+    for e, b in enumerate(blobs):
+        ptrs[e] = b.ctypes.data
+    x = O.gen_x(SEED, inst, T)
+    total, calls = 0.0, 0
+    while calls == 0 or total < budget_s:
+        sec, _ = O.baseline_layer(x, None, L, ptrs, T, threads)
+        total += sec
+        calls += 1
+    return T * FLOP_PER_TOKEN / (total / calls) / 1e9, total / calls * 1e3, calls
 
 
 def cpu_baseline(n_distinct, budget_s, max_tokens, threads):
@@ -167,6 +213,8 @@ def main():
     ap.add_argument("--graph", action="store_true", help="replay a captured HIP graph (one launch per step anyway)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-decode", action="store_true",
+                    help="skip the decode lines (profiling the prefill kernels alone); no headline value")
     ap.add_argument("--prefill-configs", default="3,4", help="BASELINE prefill configs to run (3: 512 tokens, 4: 8192)")
     ap.add_argument("--cpu-layers", type=int, default=8, help="distinct synthetic layers cycled by the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="timed CPU work of the baseline sample")
@@ -203,88 +251,118 @@ def main():
 
     stream = torch.cuda.current_stream()
 
-    # ---------------- config 2: 40-layer decode, B=1 ----------------
-    log("building 40-layer arena (18.12 GB) from the seeded generator")
-    m = qe_moe.MoE(n_layers=N_LAYERS, t_max=8)
-    for l in range(N_LAYERS):
-        m.synth_layer(l, SEED, None, stream=stream)
-    x = torch.empty(1, 2048, device=dev)
-    qe_moe.synth_x(SEED, 0, x, x.numel(), stream=stream)
-    y = torch.empty_like(x)
-    torch.cuda.synchronize()
-
-    def step_eager():
-        m.forward_stack(0, N_LAYERS, x, y, 1, stream=torch.cuda.current_stream())
-
-    step_eager()
-    torch.cuda.synchronize()
-    y_eager = y.clone()
-    step = step_eager
-    graph_used = False
-    if args.graph:
-        g = torch.cuda.CUDAGraph()
-        s = torch.cuda.Stream()
-        s.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(s):
-            step_eager()
-        torch.cuda.current_stream().wait_stream(s)
+    dec = None
+    if not args.no_decode:
+        # ---------------- config 2: 40-layer decode, B=1 ----------------
+        log("building 40-layer arena (18.12 GB) from the seeded generator")
+        m = qe_moe.MoE(n_layers=N_LAYERS, t_max=8)
+        for l in range(N_LAYERS):
+            m.synth_layer(l, SEED, None, stream=stream)
+        x = torch.empty(1, 2048, device=dev)
+        qe_moe.synth_x(SEED, 0, x, x.numel(), stream=stream)
+        y = torch.empty_like(x)
         torch.cuda.synchronize()
-        with torch.cuda.graph(g):
-            step_eager()
-        ok = True
-        for _ in range(3):  # every replay must equal the eager result
-            y.zero_()
-            g.replay()
-            torch.cuda.synchronize()
-            ok = ok and torch.equal(y, y_eager)
-            step_eager()
-            torch.cuda.synchronize()
-        if ok:
-            step, graph_used = g.replay, True
-        else:
-            log("graph replay differs from eager: timing eager launches")
-    log(f"decode: warmup {args.warmup}, timed {args.steps} (graph={graph_used})")
-    for _ in range(args.warmup):
-        step()
-    ms = timed(torch, step, args.steps, torch.cuda.current_stream())
-    tok_s = 1000.0 / ms
-    assert torch.equal(y, y_eager), "timed output differs from the eager reference"
 
-    # per-kernel HIP events over a profiled pass of the same workload (eager launches)
-    m.profile(True)
-    prof_steps = min(args.steps, 20)
-    for _ in range(prof_steps):
+        def step_eager():
+            m.forward_stack(0, N_LAYERS, x, y, 1, stream=torch.cuda.current_stream())
+
         step_eager()
-    torch.cuda.synchronize()
-    prof = m.profile_read()
-    m.profile(False)
-    dec_ms, dec_n = prof["k_decode"]
-    dec_avg_s = dec_ms / dec_n / 1e3
-    dec_bytes = N_LAYERS * LAYER_BYTES_B1  # one launch = one token through all 40 layers
-    achieved = dec_bytes / dec_avg_s
-    kernels = {k: {"avg_us": round(v[0] / v[1] * 1e3, 3), "launches": v[1]} for k, v in prof.items()}
+        torch.cuda.synchronize()
+        y_eager = y.clone()
+        step = step_eager
+        graph_used = False
+        if args.graph:
+            g = torch.cuda.CUDAGraph()
+            s = torch.cuda.Stream()
+            s.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(s):
+                step_eager()
+            torch.cuda.current_stream().wait_stream(s)
+            torch.cuda.synchronize()
+            with torch.cuda.graph(g):
+                step_eager()
+            ok = True
+            for _ in range(3):  # every replay must equal the eager result
+                y.zero_()
+                g.replay()
+                torch.cuda.synchronize()
+                ok = ok and torch.equal(y, y_eager)
+                step_eager()
+                torch.cuda.synchronize()
+            if ok:
+                step, graph_used = g.replay, True
+            else:
+                log("graph replay differs from eager: timing eager launches")
+        log(f"decode: warmup {args.warmup}, timed {args.steps} (graph={graph_used})")
+        for _ in range(args.warmup):
+            step()
+        ms = timed(torch, step, args.steps, torch.cuda.current_stream())
+        tok_s = 1000.0 / ms
+        assert torch.equal(y, y_eager), "timed output differs from the eager reference"
 
-    # batched decode, 8 tokens per step through the same 40 layers (the T <= 8 kernel)
-    x8 = torch.empty(8, 2048, device=dev)
-    qe_moe.synth_x(SEED, 1, x8, x8.numel(), stream=stream)
-    y8 = torch.empty_like(x8)
-    step8 = lambda: m.forward_stack(0, N_LAYERS, x8, y8, 8, stream=torch.cuda.current_stream())  # noqa: E731
-    for _ in range(5):
-        step8()
-    ms8 = timed(torch, step8, max(20, args.steps // 4), torch.cuda.current_stream())
-    decode_b8 = {"tokens_per_s": round(8000.0 / ms8, 1), "ms_per_step": round(ms8, 4),
-                 "note": "8 tokens per step through the 40-layer stack, no bias (independent tokens)"}
-    del m
-    torch.cuda.empty_cache()
+        # one step is one k_decode launch, so the timed region's time per step is the
+        # kernel's average launch duration (back-to-back launches on one stream)
+        dec_avg_s = ms / 1e3
+        dec_bytes = N_LAYERS * LAYER_BYTES_B1  # one launch = one token through all 40 layers
+        achieved = dec_bytes / dec_avg_s
+        # per-kernel HIP events (the library's profiler) over a short pass, for reference
+        m.profile(True)
+        for _ in range(min(args.steps, 20)):
+            step_eager()
+        torch.cuda.synchronize()
+        prof = m.profile_read()
+        m.profile(False)
+        kernels = {k: {"avg_us": round(v[0] / v[1] * 1e3, 3), "launches": v[1]} for k, v in prof.items()}
+
+        # config 0: one layer, B=1, rotated over the 40 resident layers
+        x1 = torch.empty(1, 2048, device=dev)
+        qe_moe.synth_x(SEED, 10, x1, x1.numel(), stream=stream)
+        y1 = torch.empty_like(x1)
+        ms0 = layer_rotation(torch, m, x1, y1, 1, N_LAYERS, max(200, args.steps))
+        cfg0 = {"us_per_call": round(ms0 * 1e3, 3), "tokens_per_s": round(1000.0 / ms0, 1),
+                "algorithmic_bytes": LAYER_BYTES_B1, "gbs": round(LAYER_BYTES_B1 / (ms0 / 1e3) / 1e9, 2),
+                "hbm_frac": round(LAYER_BYTES_B1 / (ms0 / 1e3) / HBM_PEAK, 4),
+                "note": "one launch per call (forward_normed, k_decode over 1 layer), calls cycle over 40 layers "
+                        "(18.1 GB, beyond the 256 MB MALL); includes the per-launch fixed cost"}
+
+        # batched decode, 8 tokens per step through the same 40 layers (the T <= 8 kernel)
+        x8 = torch.empty(8, 2048, device=dev)
+        qe_moe.synth_x(SEED, 1, x8, x8.numel(), stream=stream)
+        y8 = torch.empty_like(x8)
+        step8 = lambda: m.forward_stack(0, N_LAYERS, x8, y8, 8, stream=torch.cuda.current_stream())  # noqa: E731
+        for _ in range(5):
+            step8()
+        ms8 = timed(torch, step8, max(20, args.steps // 4), torch.cuda.current_stream())
+        stack40_b8 = {"tokens_per_s": round(8000.0 / ms8, 1), "ms_per_step": round(ms8, 4),
+                      "note": "8 tokens per step through the 40-layer stack, no router bias (not BASELINE config 1)"}
+
+        # config 1: one layer, B=8, Zipf s=1 router bias, rotated over the 40 layers
+        for l in range(N_LAYERS):
+            m.set_dense(l, bias=qe_moe.synth_zipf_bias(SEED, l, 1.0), stream=stream)
+        x8b = torch.empty(8, 2048, device=dev)
+        qe_moe.synth_x(SEED, 11, x8b, x8b.numel(), stream=stream)
+        uniq = []
+        for l in range(N_LAYERS):
+            m.forward_normed(l, x8b, y8, 8, stream=stream)
+            uniq.append(int(np.count_nonzero(np.diff(m.routing(8, stream=stream)["off"]))))
+        ms1 = layer_rotation(torch, m, x8b, y8, 8, N_LAYERS, max(200, args.steps))
+        b1 = float(np.mean(uniq)) * EXPERT_BYTES + 5447680 + 131072
+        cfg1 = {"us_per_call": round(ms1 * 1e3, 3), "tokens_per_s": round(8000.0 / ms1, 1),
+                "distinct_experts_mean": round(float(np.mean(uniq)), 2), "distinct_experts_min_max": [min(uniq), max(uniq)],
+                "algorithmic_bytes_mean": int(b1), "gbs": round(b1 / (ms1 / 1e3) / 1e9, 2),
+                "hbm_frac": round(b1 / (ms1 / 1e3) / HBM_PEAK, 4),
+                "note": "bytes = U x 1,769,472 (each distinct expert once) + 5,447,680 dense + 131,072 activations; "
+                        "one launch per call, calls cycle over 40 layers with per-layer Zipf(1.0) biases"}
+        del m
+        torch.cuda.empty_cache()
+        dec = dict(tok_s=tok_s, ms=ms, graph_used=graph_used, dec_avg_s=dec_avg_s, dec_bytes=dec_bytes,
+                   achieved=achieved, kernels=kernels, cfg0=cfg0, cfg1=cfg1, stack40_b8=stack40_b8)
 
     # ---------------- config 3: prefill 512, one layer ----------------
     pre = {}
     pcfg = set() if args.no_prefill else {c.strip() for c in args.prefill_configs.split(",")}
-    if pcfg:
-        sys.path.insert(0, os.path.join(REPO, "oracle"))
-        import oracle as O
     if "3" in pcfg:
-        bias = O.gen_zipf_bias(SEED, 0, 1.0)
+        bias = qe_moe.synth_zipf_bias(SEED, 0, 1.0)
         mp = qe_moe.MoE(n_layers=1, t_max=512)
         mp.synth_layer(0, SEED, bias, stream=stream)
         xp = torch.empty(512, 2048, device=dev)
@@ -331,7 +409,7 @@ def main():
         # config 4: prefill 8192, one layer, Zipf s=1.3 router bias
         T4 = 8192
         m4 = qe_moe.MoE(n_layers=1, t_max=T4)
-        m4.synth_layer(0, SEED, O.gen_zipf_bias(SEED, 0, 1.3), stream=stream)
+        m4.synth_layer(0, SEED, qe_moe.synth_zipf_bias(SEED, 0, 1.3), stream=stream)
         x4 = torch.empty(T4, 2048, device=dev)
         qe_moe.synth_x(SEED, 4, x4, x4.numel(), stream=stream)
         y4 = torch.empty_like(x4)
@@ -348,6 +426,20 @@ def main():
                                      "experts_lt4_tokens": int(((c4 > 0) & (c4 < 4)).sum())}
         del m4, x4, y4
         torch.cuda.empty_cache()
+
+    if not args.no_cpu_baseline:
+        for key, T_, inst, s_ in (("prefill512", 512, 3, 1.0), ("prefill8192_zipf13", 8192, 4, 1.3)):
+            if (key == "prefill512" and "3" not in pcfg) or (key != "prefill512" and "4" not in pcfg):
+                continue
+            log(f"cpu baseline: {key}")
+            gf, cms, ncall = cpu_prefill(T_, inst, s_, threads, args.cpu_seconds / 2)
+            entry = {"value": round(gf, 2), "unit": "GFLOP/s", "ms_per_call": round(cms, 1), "cores": threads,
+                     "kind": "port", "sample": f"{ncall} call(s) of the same {T_}-token layer (all 256 experts), "
+                                               "the reference's batched CPU expert path"}
+            if key == "prefill512":
+                pre["prefill512_cpu_baseline"] = entry
+            else:
+                pre[key]["cpu_baseline"] = entry
 
     conv = None
     if not args.no_convert:
@@ -373,12 +465,16 @@ def main():
             pass
 
     traffic = pmc_traffic(os.path.join(REPO, TRAFFIC_FILE))
+    if dec is None:  # prefill-only run (profiling): no headline line
+        print(json.dumps({**pre, "convert_layer_q8_0": conv, "cpu_baseline": cpu}), flush=True)
+        return
+    tok_s, ms, achieved, dec_avg_s, dec_bytes = dec["tok_s"], dec["ms"], dec["achieved"], dec["dec_avg_s"], dec["dec_bytes"]
     out = {
         "metric": METRIC, "value": round(tok_s, 2), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "int8", "data": "synthetic (seeded random-init weights of the config shapes)",
         "config": {"workload": "cfg2: 40-layer MoE-only stack, decode B=1, 1 token per step", "layers": N_LAYERS,
-                   "tokens_per_step": 1, "experts": 256, "top_k": 8, "hip_graph": graph_used},
+                   "tokens_per_step": 1, "experts": 256, "top_k": 8, "hip_graph": dec["graph_used"]},
         "hbm_gbs": round(N_LAYERS * LAYER_BYTES_B1 * tok_s / 1e9, 2),
         "hbm_frac": round(N_LAYERS * LAYER_BYTES_B1 * tok_s / HBM_PEAK, 4),
         **pre,
@@ -387,9 +483,12 @@ def main():
                      "frac": round(achieved / HBM_PEAK, 4),
                      "traffic": None if traffic is None else round(traffic), "traffic_source": TRAFFIC_FILE,
                      "bytes_per_launch": dec_bytes,
-                     "avg_us": round(dec_avg_s * 1e6, 3)},
-        "kernels": kernels,
-        "decode_b8": decode_b8,
+                     "avg_us": round(dec_avg_s * 1e6, 3),
+                     "avg_us_source": "timed region / steps (one k_decode launch per step, HIP events on its stream)"},
+        "kernels": dec["kernels"],
+        "cfg0_decode_b1_layer": dec["cfg0"],
+        "cfg1_decode_b8_zipf_layer": dec["cfg1"],
+        "stack40_b8": dec["stack40_b8"],
         "convert_layer_q8_0": conv,
         "cpu_baseline": cpu,
     }

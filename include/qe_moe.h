@@ -179,6 +179,10 @@ int qe_moe_arena_ptr(qe_moe_ctx *ctx, int layer, void **dev);
 int qe_moe_synth_layer(qe_moe_ctx *ctx, int layer, uint64_t seed, const float *bias, void *stream);
 /* Fill n fp32 activations N(0,1) of activation set `inst` on the device. */
 int qe_moe_synth_x(uint64_t seed, int inst, float *dev_out, int64_t n, void *stream);
+/* The benchmark router bias of a layer (host fp32[256]): b_e = -s * ln(rank_e)
+ * over a seeded permutation of the ranks 1..256, i.e. log Zipf(s) popularity
+ * (3, 4).  Host only, no device work. */
+int qe_moe_synth_zipf_bias(uint64_t seed, int layer, double s, float *out);
 
 /* Decode poll timeouts.  The T <= 8 path synchronises workgroups through
  * bounded polls; a poll that gives up (a hung or starved peer) lets the

@@ -622,6 +622,12 @@ int qe_moe_synth_layer(qe_moe_ctx *c, int layer, uint64_t seed, const float *bia
     return QE_OK;
 }
 
+int qe_moe_synth_zipf_bias(uint64_t seed, int layer, double s, float *out) {
+    if (!out || !(s >= 0.0)) return fail(QE_ERR_ARG, "synth_zipf_bias: bad argument");
+    qe_synth_zipf_bias(seed, layer, s, out);
+    return QE_OK;
+}
+
 int qe_moe_synth_x(uint64_t seed, int inst, float *dev_out, int64_t n, void *stream) {
     if (!dev_out || n < 0) return fail(QE_ERR_ARG, "synth_x: bad argument");
     if (n == 0) return QE_OK;

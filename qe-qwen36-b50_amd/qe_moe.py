@@ -82,6 +82,7 @@ def load(path: str = LIB_PATH):
         "qe_moe_load_pack": (i32, [vp, ctypes.c_char_p, i32, i32, i32, vp]),
         "qe_moe_synth_layer": (i32, [vp, i32, u64, vp, vp]),
         "qe_moe_synth_x": (i32, [u64, i32, vp, i64, vp]),
+        "qe_moe_synth_zipf_bias": (i32, [u64, i32, ctypes.c_double, vp]),
         "qe_moe_last_error": (ctypes.c_char_p, []),
         "qe_moe_profile": (i32, [vp, i32]),
         "qe_moe_profile_read": (i32, [vp, vp, vp, i32]),
@@ -225,6 +226,14 @@ class MoE:
         lg = np.empty((T, ROUTER_ROWS), np.float32)
         _check(_lib.qe_moe_get_logits(self.h, T, _ptr(lg), _stream(stream)))
         return lg
+
+
+def synth_zipf_bias(seed, layer, s):
+    """Host fp32[256] router bias -s * ln(rank) over a seeded permutation of the ranks (benchmark set-up)."""
+    load()
+    out = np.empty(N_EXPERT, np.float32)
+    _check(_lib.qe_moe_synth_zipf_bias(seed, layer, float(s), _ptr(out)))
+    return out
 
 
 def synth_x(seed, inst, dev_out, n, stream=None):
