@@ -110,7 +110,8 @@ int qe_moe_get_routing(qe_moe_ctx *ctx, int T, int32_t *ids, float *wts, float *
                        float *shared_out, void *stream);
 
 /* Token-to-expert dispatch alone on caller-supplied ids (device int32[T][8],
- * each in 0..255): per-expert histogram, exclusive scan and the stable
+ * each in 0..255; the kernels reduce other values modulo 256, so a bad id
+ * yields a wrong permutation but no out-of-bounds access): per-expert histogram, exclusive scan and the stable
  * permutation of Engine::moe_batched (engine/qe.cpp:1965-1976), run on the
  * GPU; read the result with qe_moe_get_routing (off, pairs). */
 int qe_moe_dispatch(qe_moe_ctx *ctx, const int32_t *ids, int T, void *stream);

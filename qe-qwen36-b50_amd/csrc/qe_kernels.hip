@@ -113,7 +113,7 @@ __global__ __launch_bounds__(1024) void k_disp_hist(const int32_t *ids, int np, 
     const int tid = threadIdx.x, p = blockIdx.x * 1024 + tid;
     if (tid < QE_N_EXPERT) h[tid] = 0;
     __syncthreads();
-    if (p < np) atomicAdd(&h[ids[p]], 1);
+    if (p < np) atomicAdd(&h[ids[p] & (QE_N_EXPERT - 1)], 1); // ids are 0..255; others reduce modulo 256, in bounds
     __syncthreads();
     if (tid < QE_N_EXPERT) chunk_hist[blockIdx.x * QE_N_EXPERT + tid] = h[tid];
 }
@@ -202,7 +202,7 @@ __global__ __launch_bounds__(1024) void k_disp_scatter(const int32_t *ids, int n
     }
     const int p = blockIdx.x * 1024 + tid;
     const bool valid = p < np;
-    const int e = valid ? ids[p] : 0;
+    const int e = valid ? ids[p] & (QE_N_EXPERT - 1) : 0; // as k_disp_hist
     unsigned long long peers = __ballot(valid);
 #pragma unroll
     for (int bit = 0; bit < 8; ++bit) {
