@@ -116,6 +116,21 @@ int qe_moe_get_routing(qe_moe_ctx *ctx, int T, int32_t *ids, float *wts, float *
  * GPU; read the result with qe_moe_get_routing (off, pairs). */
 int qe_moe_dispatch(qe_moe_ctx *ctx, const int32_t *ids, int T, void *stream);
 
+/* qe_moe_dispatch without a context and without allocating: the same
+ * histogram / scan / stable permutation (results identical to
+ * qe_moe_dispatch followed by qe_moe_get_routing's off and pairs), written to
+ * the caller's device buffers off int32[257] and pairs int32[T*8], on the
+ * calling thread's current device.  No reference counterpart: it is for
+ * callers that cannot call hipMalloc (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid allocation).  Its scratch (chunk
+ * histograms and work items, about 200 KB) is a static device array the
+ * library holds on every device it runs on until the process ends, sized for
+ * T <= QE_MOE_DISPATCH_NOALLOC_T_MAX; larger T returns QE_ERR_ARG.  Every call
+ * on one device shares that array: calls that overlap on one device (other
+ * streams, other threads) race. */
+#define QE_MOE_DISPATCH_NOALLOC_T_MAX 16384
+int qe_moe_dispatch_noalloc(const int32_t *ids, int T, int32_t *off, int32_t *pairs, void *stream);
+
 /* Router logits fp32[T][257] of the last forward call (synchronises `stream`,
  * copies to host): the parity sink of the reference's RL buffer
  * (engine/qe.cpp:1959). */

@@ -462,6 +462,16 @@ int qe_moe_dispatch(qe_moe_ctx *c, const int32_t *ids, int T, void *stream) {
     return QE_OK;
 }
 
+int qe_moe_dispatch_noalloc(const int32_t *ids, int T, int32_t *off, int32_t *pairs, void *stream) {
+    if (!ids || !off || !pairs) return fail(QE_ERR_ARG, "dispatch_noalloc: null pointer");
+    if (T < 1 || T > QE_MOE_DISPATCH_NOALLOC_T_MAX)
+        return fail(QE_ERR_ARG, "dispatch_noalloc: T=%d outside 1..%d (the static scratch's size)", T,
+                    QE_MOE_DISPATCH_NOALLOC_T_MAX);
+    HIP_TRY(qe_launch_dispatch_noalloc(ids, T, off, pairs, (hipStream_t)stream));
+    return QE_OK;
+}
+static_assert(QE_MOE_DISPATCH_NOALLOC_T_MAX == QE_DISPATCH_NOALLOC_T_MAX, "header and library limits agree");
+
 int qe_moe_get_logits(qe_moe_ctx *c, int T, float *logits, void *stream) {
     if (!c || !logits || T <= 0 || T > c->t_max) return fail(QE_ERR_ARG, "get_logits: bad argument");
     HIP_TRY(hipSetDevice(c->device));

@@ -103,6 +103,10 @@ hipError_t qe_launch_layer(const QeLayerPtrs &L, const QeScratch &S, const float
                            float *out, int T, hipStream_t st, const float *exit_norm = nullptr,
                            float *exit_xn = nullptr);
 hipError_t qe_launch_dispatch(const QeScratch &S, int T, hipStream_t st);
+// The same dispatch with its scratch in a static device array (no allocation);
+// off and pairs are the caller's device buffers.
+#define QE_DISPATCH_NOALLOC_T_MAX 16384
+hipError_t qe_launch_dispatch_noalloc(const int32_t *ids, int T, int32_t *off, int32_t *pairs, hipStream_t st);
 hipError_t qe_launch_expert_mfma(const QeLayerPtrs &L, const QeScratch &S, int T, hipStream_t st);
 hipError_t qe_launch_router_shgu(const QeLayerPtrs &L, const QeScratch &S, int T, hipStream_t st);
 

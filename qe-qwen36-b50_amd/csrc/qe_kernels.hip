@@ -9,6 +9,8 @@
 // Routing (RMSNorm, router dot products, top-8) follows the checker's
 // canonical fp32 order exactly; expert products use exact int8 block dots
 // with fp32 block scaling, so they agree with the CPU path to fp32 rounding.
+#include <mutex>
+
 #include "qe_kernels.h"
 
 // ===========================================================================
@@ -365,6 +367,53 @@ hipError_t qe_launch_dispatch(const QeScratch &S, int T, hipStream_t st) {
     k_disp_hist<<<nch, 1024, 0, st>>>(S.ids, np, S.chunk_hist);
     k_disp_scatter<<<nch, 1024, 0, st>>>(S.ids, np, S.chunk_hist, nch, QE_MFMA_MC, S.off, S.pairs, S.items,
                                           S.n_items);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Dispatch without allocation: the scratch of the two dispatch kernels (the
+// per-chunk histograms and the work items) lives in a file-scope device array
+// instead of a context.  Host code never passes `scratch` itself (in host code
+// the name is a stand-in, not a device address): the first call on a device
+// looks the array's address up with hipGetSymbolAddress, with that device
+// current, and every launch on that device takes the looked-up pointer.
+// Nothing in it needs zeroing: k_disp_hist writes every histogram entry the
+// scatter reads, and the scatter writes the items.  Every call on a device
+// shares its array, so calls that overlap on one device race.
+// ---------------------------------------------------------------------------
+#define NOALLOC_NCH (QE_DISPATCH_NOALLOC_T_MAX * QE_K_USED / 1024)
+#define NOALLOC_ITEMS (QE_DISPATCH_NOALLOC_T_MAX * QE_K_USED / (QE_MFMA_MC / 2 + 1) + 1 + QE_N_EXPERT)
+#define NOALLOC_HIST_BYTES ((size_t)NOALLOC_NCH * QE_N_EXPERT * 4)
+#define NOALLOC_BYTES (NOALLOC_HIST_BYTES + (size_t)NOALLOC_ITEMS * 16 + 256)
+static_assert(NOALLOC_HIST_BYTES % 256 == 0, "items start 256-byte aligned");
+static __device__ __align__(256) uint8_t scratch[NOALLOC_BYTES];
+
+#define NOALLOC_MAX_DEV 64
+static std::mutex g_noalloc_mu;
+static void *g_noalloc_ptr[NOALLOC_MAX_DEV];
+
+hipError_t qe_launch_dispatch_noalloc(const int32_t *ids, int T, int32_t *off, int32_t *pairs, hipStream_t st) {
+    if (T < 1 || T > QE_DISPATCH_NOALLOC_T_MAX) return hipErrorInvalidValue;
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= NOALLOC_MAX_DEV) return hipErrorInvalidDevice;
+    uint8_t *base;
+    {
+        std::lock_guard<std::mutex> lk(g_noalloc_mu);
+        if (!g_noalloc_ptr[dev]) {
+            void *p = nullptr;
+            if ((e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch))) != hipSuccess) return e;
+            g_noalloc_ptr[dev] = p;
+        }
+        base = (uint8_t *)g_noalloc_ptr[dev];
+    }
+    int32_t *chunk_hist = (int32_t *)base;
+    int4 *items = (int4 *)(base + NOALLOC_HIST_BYTES);
+    int32_t *n_items = (int32_t *)(base + NOALLOC_HIST_BYTES + (size_t)NOALLOC_ITEMS * 16);
+    const int np = T * QE_K_USED, nch = (np + 1023) / 1024;
+    k_disp_hist<<<nch, 1024, 0, st>>>(ids, np, chunk_hist);
+    k_disp_scatter<<<nch, 1024, 0, st>>>(ids, np, chunk_hist, nch, QE_MFMA_MC, off, pairs, items, n_items);
     return hipGetLastError();
 }
 

@@ -35,6 +35,7 @@ NPROF = 11
 # ggml type ids of converter sources (QE_SRC_* in the header)
 SRC_F32, SRC_F16, SRC_Q8_0, SRC_BF16 = 0, 1, 8, 30
 QE_OK, QE_ERR_ARG, QE_ERR_HIP, QE_ERR_OOM, QE_ERR_STATE = 0, -1, -2, -3, -4
+QE_MOE_DISPATCH_NOALLOC_T_MAX = 16384  # include/qe_moe.h
 
 
 class LibraryMissing(RuntimeError):
@@ -90,6 +91,7 @@ def load(path: str = LIB_PATH):
         "qe_moe_nl4_quantize_rows": (i32, [vp, i32, i64, i32, vp, vp]),
         "qe_moe_convert_experts": (i32, [vp, i32, vp, vp, vp, i32, vp]),
         "qe_moe_check": (i32, [vp, vp]),
+        "qe_moe_dispatch_noalloc": (i32, [vp, i32, vp, vp, vp]),
         "qe_moe_debug_set_epoch": (i32, [vp, ctypes.c_uint32, vp]),
         "qe_moe_debug_set_spin_cap": (i32, [vp, i32]),
     }
@@ -226,6 +228,12 @@ class MoE:
         lg = np.empty((T, ROUTER_ROWS), np.float32)
         _check(_lib.qe_moe_get_logits(self.h, T, _ptr(lg), _stream(stream)))
         return lg
+
+
+def dispatch_noalloc(ids_dev, T, off_dev, pairs_dev, stream=None):
+    """Context-free dispatch into caller buffers (no allocation; scratch in a static device array)."""
+    load()
+    _check(_lib.qe_moe_dispatch_noalloc(_ptr(ids_dev), T, _ptr(off_dev), _ptr(pairs_dev), _stream(stream)))
 
 
 def synth_zipf_bias(seed, layer, s):
