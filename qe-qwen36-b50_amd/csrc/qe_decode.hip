@@ -1,6 +1,14 @@
 // Persistent decode kernel: T <= 8 tokens through n_layers MoE layers in ONE
-// cooperative launch (the MoE sections of Engine::decode, engine/qe.cpp:2466-2572,
-// and decode_multi<NT>, :1653-1737, looped over the layers as at :2241).
+// launch (the MoE sections of Engine::decode, engine/qe.cpp:2466-2572, and
+// decode_multi<NT>, :1653-1737, looped over the layers as at :2241).
+//
+// Its workgroups wait for each other, so all of them must be resident at once:
+// one per CU (the LDS use admits no second), at most as many as there are
+// CUs.  A plain launch of that grid on an otherwise idle device puts every
+// workgroup on its own CU; hipLaunchCooperativeKernel guarantees the same but
+// measured 18 us more per launch (37 against 19 us for one layer).  Should
+// another kernel hold CUs, the late workgroups start when it ends; the polls
+// are bounded either way, and a timeout is reported to the caller.
 //
 // Why persistent: on MI355X every kernel launch costs ~4.5 us of fixed
 // duration (dispatch over 8 XCDs + end-of-kernel L2 write-back), while one
@@ -74,7 +82,9 @@ QE_DEV int xpos(int e) { return (e & 31) * 65 + (e >> 5); } // raw x element e o
 #define L_MISC (L_SHG + 8 * 4)                      // int [16]
 #define L_INV (L_MISC + 16 * 4)                     // f32 [8]          1 / rms of each token
 #define L_SD (L_INV + 8 * 4)                        // f32 [4][8][T]    shared-expert output of the D rows
-#define L_TOTAL (L_SD + 4 * 8 * DEC_T * 4)
+#define L_TK (L_SD + 4 * 8 * DEC_T * 4)            // T = 1 top-8: u64 [256] survivor order keys, int [256] their
+                                                    //   experts, u32 [8] logit keys by rank, f32 logit 256
+#define L_TOTAL (L_TK + 256 * 8 + 256 * 4 + 8 * 4 + 16)
 static_assert(L_Y + 8 * 2 * DEC_T * 4 <= L_U_END, "D-stage LDS must fit in the union");
 static_assert(64 * 8 * 4 <= L_HQ - L_U, "G-stage LDS must fit in front of the D buffers");
 static_assert(L_TOTAL <= 160 * 1024, "LDS budget of one workgroup per CU");
@@ -228,9 +238,13 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
         // The first row task of waves 0..3 is copied into LDS before waiting for x
         // (global->LDS, no registers held): a router row as 2048 fp32, or a shared
         // (gate, up) pair as 2 x 2048 int8 + 2 x 64 scales, one u16 per dword.
-        const int task0 = blockIdx.x + (int)gridDim.x * wv;
-        uint8_t *rw_lds = lds + L_RW + (wv & 3) * 8192;
-        const bool rw_pref = wv < 4 && task0 < N_RTASK;
+        // T = 1: wave 0 takes no row task; it polls the logits next, and a poll
+        // issued after a store of its own would wait for that store's
+        // acknowledgement as well (vmcnt counts both).
+        constexpr int TW0 = TM == 1 ? 1 : 0;  // first wave with row tasks
+        const int task0 = wv < TW0 ? N_RTASK : blockIdx.x + (int)gridDim.x * (wv - TW0);
+        uint8_t *rw_lds = lds + L_RW + ((wv - TW0) & 3) * 8192;
+        const bool rw_pref = wv >= TW0 && wv < TW0 + 4 && task0 < N_RTASK;
         if (rw_pref) {
             // Lane i's 16 bytes land at dst + 16 i; the source is the i-th lane chunk's
             // k-th 16 bytes, so the dot (lane = chunk) reads dst + 16 lane: no bank conflicts.
@@ -335,7 +349,7 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
             }
         }
         __syncthreads();
-        for (int task = task0; task < N_RTASK; task += (int)gridDim.x * NWV) {
+        for (int task = task0; task < N_RTASK; task += (int)gridDim.x * (NWV - TW0)) {
             const bool in_lds = rw_pref && task == task0;
             if (task < QE_ROUTER_ROWS) {
                 const bool add_bias = bias && task < QE_N_EXPERT;
@@ -394,7 +408,86 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
         }
 
         // ================= G: top-8, dispatch, routed gate/up =================
-        if (wv < T) {
+        if constexpr (TM == 1) {
+            // Top-8 by one wave, lane l holding the logits of experts l + 64 j.  A
+            // lane's maximum over its four, then over groups of 8 lanes, gives eight
+            // maxima of distinct experts; the smallest of them bounds the 8th largest
+            // logit from below, so the experts at or above it (about 18 of 256) hold
+            // the top 8.  Each of these survivors counts the survivors ahead of it in
+            // the reference's total order (larger value first, ties to the smaller
+            // (e % 16, e / 16)), one 64-bit comparison of {ordered value, 0xffff -
+            // tie key} each: ranks 0..7 are the selection in order.  The experts
+            // become the items in rank order; the weights are formed later, off the
+            // critical path (they are first needed in D).  (Rounds of wave maxima, or
+            // the ranks counted by every thread over all 256, took 1-2 us per layer.)
+            uint64_t *s_sk = (uint64_t *)(lds + L_TK);           // [256] survivors' order keys
+            int *s_se = (int *)(lds + L_TK + 2048);                // [256] survivors' experts
+            unsigned *s_rkey = (unsigned *)(lds + L_TK + 3072);    // [8] logit keys by rank
+            float *s_lg256 = (float *)(lds + L_TK + 3104);
+            if (wv == 0) {
+                uint64_t w[5]; // the lane's four logits and (lane 0) logit 256, one poll loop
+                for (int spins = 0;; ++spins) {
+                    unsigned bad = 0;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        w[j] = LD_A((uint64_t *)EXr + EX_L + lane + 64 * j);
+                        bad |= (unsigned)(w[j] >> 32) ^ tagR;
+                    }
+                    w[4] = lane == 0 ? LD_A((uint64_t *)EXr + EX_L + QE_N_EXPERT) : ((uint64_t)tagR << 32);
+                    bad |= (unsigned)(w[4] >> 32) ^ tagR;
+                    if (__all(bad == 0)) break;
+                    if (spins + 1 >= pc.cap) { poll_timeout(pc); break; }
+                    __builtin_amdgcn_s_sleep(1);
+                }
+                unsigned v[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) v[j] = f2ord(tv_val(w[j]) + 0.0f);
+                if (lane == 0) *s_lg256 = tv_val(w[4]);
+                if (last && blockIdx.x == 0) {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) a.logits[lane + 64 * j] = tv_val(w[j]);
+                    if (lane == 0) a.logits[QE_N_EXPERT] = tv_val(w[4]);
+                }
+                unsigned g = umax32(umax32(v[0], v[1]), umax32(v[2], v[3]));
+                g = umax32(g, dpp_ub<QE_DPP_XOR1>(g));
+                g = umax32(g, dpp_ub<QE_DPP_XOR2>(g));
+                g = umax32(g, dpp_ub<QE_DPP_HMIRROR>(g)); // maximum of 32 experts (8 lanes)
+                g = umin32(g, dpp_ub<QE_DPP_MIRROR>(g));
+                unsigned ra, rb;
+                rows16(g, ra, rb);
+                g = umin32(ra, rb);
+                rows32(g, ra, rb);
+                g = umin32(ra, rb); // the smallest of the eight
+                int S = 0;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) { // survivors numbered by (j, lane)
+                    const bool sv = v[j] >= g;
+                    const unsigned long long bal = __ballot(sv);
+                    if (sv) {
+                        const int e = lane + 64 * j, pos = S + (int)__builtin_amdgcn_mbcnt_hi((unsigned)(bal >> 32), __builtin_amdgcn_mbcnt_lo((unsigned)bal, 0u));
+                        s_sk[pos] = ((uint64_t)v[j] << 32) | (0xffffu - (unsigned)((e & 15) * 16 + (e >> 4)));
+                        s_se[pos] = e;
+                    }
+                    S += (int)__popcll(bal);
+                }
+                for (int i0 = 0; i0 < S; i0 += 64) { // more than 64 survivors only with many equal logits
+                    const int i = i0 + lane;
+                    const uint64_t ki = s_sk[i < S ? i : 0];
+                    int r = 0, j = 0;
+                    for (; j + 4 <= S; j += 4) {
+                        const uint64_t k0 = s_sk[j], k1 = s_sk[j + 1], k2 = s_sk[j + 2], k3 = s_sk[j + 3];
+                        r += (int)(k0 > ki) + (int)(k1 > ki) + (int)(k2 > ki) + (int)(k3 > ki);
+                    }
+                    for (; j < S; ++j) r += (int)(s_sk[j] > ki);
+                    if (i < S && r < QE_K_USED) {
+                        s_items[r] = make_int4(s_se[i] & (QE_N_EXPERT - 1), r, 1, 0);
+                        s_rkey[r] = (unsigned)(ki >> 32);
+                    }
+                }
+                if (lane < QE_K_USED) s_pairs[lane] = lane;
+                if (lane == 0) s_misc[0] = QE_K_USED;
+            }
+        } else if (wv < T) {
             const int t = wv;
             uint64_t w[5];
             read_tv<4>(EXr + EX_L + t * QE_ROUTER_ROWS + lane, 64, tagR, w, true, pc);
@@ -407,42 +500,7 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
                 for (int j = 0; j < 4; ++j) a.logits[t * QE_ROUTER_ROWS + lane + 64 * j] = v[j];
                 if (lane == 0) a.logits[t * QE_ROUTER_ROWS + QE_N_EXPERT] = v[4];
             }
-            const int myid = wave_topk_vals(v, v[4], lane, s_ids + t * QE_K_USED, s_wts + t * QE_K_USED, s_shg + t);
-            if (TM == 1) {
-                // one token: its 8 distinct experts are the items, in expert order
-                // (engine/qe.cpp:1965-1976 with one pair per expert): lane k < 8
-                // holds pair k's expert, and its slot is the count of smaller ids
-                // (plus equal ids of earlier pairs, so the slots stay a permutation
-                // of 0..7 even if a timed-out poll fed the top-8 garbage)
-                int id8[QE_K_USED], rank = 0;
-#pragma unroll
-                for (int j = 0; j < QE_K_USED; ++j) {
-                    id8[j] = __builtin_amdgcn_readlane(myid, j);
-                    rank += id8[j] < myid || (id8[j] == myid && j < lane);
-                }
-                if (lane < QE_K_USED) {
-                    s_pairs[rank] = lane;
-                    s_items[rank] = make_int4(myid, rank, 1, 0);
-                }
-                if (lane == 0) s_misc[0] = QE_K_USED;
-                if (last && blockIdx.x == 0) {
-                    if (lane < QE_K_USED) {
-                        a.pairs[rank] = lane;
-                        a.ids[lane] = myid;
-                        a.wts[lane] = s_wts[lane];
-                    }
-                    if (lane == 0) a.shg[0] = s_shg[0];
-#pragma unroll
-                    for (int k = 0; k < 4; ++k) { // per-expert offsets for the routing sink
-                        const int ee = lane * 4 + k;
-                        int o = 0;
-#pragma unroll
-                        for (int j = 0; j < QE_K_USED; ++j) o += id8[j] < ee;
-                        a.off[ee] = o;
-                    }
-                    if (lane == 0) a.off[QE_N_EXPERT] = QE_K_USED;
-                }
-            }
+            wave_topk_vals(v, v[4], lane, s_ids + t * QE_K_USED, s_wts + t * QE_K_USED, s_shg + t);
         }
         __syncthreads();
         if (TM != 1 && wv == 0) {
@@ -532,12 +590,52 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
         };
 
         // Units of one expert item: JU hidden rows j (gate rows j, up rows 512 + j).
-        //   mode16 (T = 1): JU = 16, 32 rows; wave w < 8 -> gate rows 2w, 2w+1, w >= 8 -> up;
-        //                   32 lanes per row, a lane holds blocks c, c + 32.  h published fp32.
+        //   mode16 (T = 1): JU = 16; wave w -> h row j0 + w: its gate row in lanes
+        //                   0..31, its up row in lanes 32..63, a lane holds blocks c,
+        //                   c + 32.  The wave forms h = silu(g) * u and publishes it
+        //                   (fp32) itself: no workgroup barrier.
         //   else:           JU = 32, 64 rows; wave w -> 4 rows, 16 lanes per row, a lane
         //                   holds blocks c + 16 i.  h quantised per 32 rows, published int8.
         const int JU = mode16 ? 16 : 32, upi = QE_FF_EXP / JU, nunits = nitems * upi;
         auto no_prefetch = []() {};
+        if constexpr (TM == 1) {
+            // The shared-expert activations (written in R) are read here, their
+            // loads in flight with the unit's, instead of on the h wait in D.
+            uint64_t hsh_w = 0;
+            if (tid < QE_FF_SH) hsh_w = LD_A((uint64_t *)EXr + EX_HSH + tid);
+            for (int unit = blockIdx.x; unit < nunits; unit += gridDim.x) {
+                const int4 it = s_items[unit / upi];
+                const int j = (unit % upi) * JU + wv, c = lane & 31;
+                const uint8_t *row = arena + (size_t)(it.x & (QE_N_EXPERT - 1)) * QE_EXPERT_BYTES +
+                                     (size_t)((lane >= 32 ? QE_FF_EXP : 0) + j) * QE_GU_ROW_BYTES;
+                const uint4 q0 = *(const uint4 *)(row + c * 16), q1 = *(const uint4 *)(row + (c + 32) * 16);
+                const uint16_t r0 = ((const uint16_t *)(row + QE_D / 2))[c], r1 = ((const uint16_t *)(row + QE_D / 2))[c + 32];
+                const float d0 = f16_bits_to_f32(r0) * s_xs[c], d1 = f16_bits_to_f32(r1) * s_xs[c + 32];
+                float acc = d0 * (float)nl4_block_dot(nl4_decode_block<true>(q0), *(const uint4 *)(s_xq + c * 32),
+                                                      *(const uint4 *)(s_xq + c * 32 + 16));
+                acc = fmaf(d1, (float)nl4_block_dot(nl4_decode_block<true>(q1), *(const uint4 *)(s_xq + (c + 32) * 32),
+                                                    *(const uint4 *)(s_xq + (c + 32) * 32 + 16)), acc);
+                acc = add_rows16(sum16(acc)); // lanes 0..31: g, lanes 32..63: u
+                const float g = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), 0));
+                const float u = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), 32));
+                const float h = silu_mul(g, u);
+                const int p = s_pairs[it.y & 7];
+                if (unit == (int)blockIdx.x && tid < QE_FF_SH) {
+                    // consumed before the publication below: a wait for a load after
+                    // a store is a wait for the store's acknowledgement too (vmcnt
+                    // counts both), ~1 us for these write-through stores
+                    uint64_t w1[1] = {hsh_w};
+                    if ((unsigned)(w1[0] >> 32) != tagR) read_tv<1>(EXr + EX_HSH + tid, 0, tagR, w1, true, pc);
+                    s_hsh[tid] = tv_val(w1[0]);
+                }
+                if (lane < REP) ST_A(EX + lane * EX_TOTAL + EX_HF + (size_t)p * QE_FF_EXP + j, pack_tv(h, tagG));
+            }
+            if ((int)blockIdx.x >= nunits && tid < QE_FF_SH) { // no unit here
+                uint64_t w1[1] = {hsh_w};
+                if ((unsigned)(w1[0] >> 32) != tagR) read_tv<1>(EXr + EX_HSH + tid, 0, tagR, w1, true, pc);
+                s_hsh[tid] = tv_val(w1[0]);
+            }
+        } else
         for (int unit = blockIdx.x; unit < nunits; unit += gridDim.x) {
             const int4 it = s_items[unit / upi];
             const int j0 = (unit % upi) * JU;
@@ -581,18 +679,53 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
             __syncthreads(); // s_gu is reused by the next unit
         }
         d_prefetch(); // workgroups without a unit
-
         // ================= D: routed down + shared down + combine =================
         // No counter: h is polled through its tags.  For T = 1 one word per unit
-        // (its last row) is polled first, then everything is read with the tags
-        // verified (a late word is re-read).
+        // (the row of its last wave) is polled first, then everything is read
+        // with the tags verified (a late word is re-read): polling all 4096 words
+        // from every workgroup would flood the memory system while it waits.
         // shared-expert activations of every token: written in R, long landed by now
-        for (int i = tid; i < T * QE_FF_SH; i += NTH) {
-            uint64_t w[1];
-            read_tv<1>(EXr + EX_HSH + i, 0, tagR, w, true, pc);
-            s_hsh[i] = tv_val(w[0]);
+        // (T = 1 read them in G)
+        if constexpr (TM != 1) {
+            for (int i = tid; i < T * QE_FF_SH; i += NTH) {
+                uint64_t w[1];
+                read_tv<1>(EXr + EX_HSH + i, 0, tagR, w, true, pc);
+                s_hsh[i] = tv_val(w[0]);
+            }
         }
         __syncthreads();
+        if (TM == 1 && wv == NWV - 1) {
+            // weights and shared gate of the selection (read after the h wait), and
+            // the routing sink of the last layer: ids by rank, pairs/off in expert
+            // order; by a wave the shared down rows leave idle
+            const unsigned *s_rkey = (const unsigned *)(lds + L_TK + 3072);
+            const int myid = lane < QE_K_USED ? s_items[lane].x & (QE_N_EXPERT - 1) : 0;
+            const float mine = ord2f(s_rkey[lane < QE_K_USED ? lane : 0]), sel0 = ord2f(s_rkey[0]);
+            topk_finish(mine, myid, sel0, *(const float *)(lds + L_TK + 3104), lane, s_ids, s_wts, s_shg);
+            if (last && blockIdx.x == 0) {
+                int id8[QE_K_USED], rank = 0;
+#pragma unroll
+                for (int jj = 0; jj < QE_K_USED; ++jj) {
+                    id8[jj] = __builtin_amdgcn_readlane(myid, jj);
+                    rank += id8[jj] < myid || (id8[jj] == myid && jj < lane);
+                }
+                if (lane < QE_K_USED) {
+                    a.pairs[rank] = lane;
+                    a.ids[lane] = myid;
+                    a.wts[lane] = s_wts[lane];
+                }
+                if (lane == 0) a.shg[0] = s_shg[0];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) { // per-expert offsets
+                    const int ee = lane * 4 + k;
+                    int o = 0;
+#pragma unroll
+                    for (int jj = 0; jj < QE_K_USED; ++jj) o += id8[jj] < ee;
+                    a.off[ee] = o;
+                }
+                if (lane == 0) a.off[QE_N_EXPERT] = QE_K_USED;
+            }
+        }
         // The shared down rows of every D row group run first, while the routed
         // h is still on its way: wave (rr, half 0), 16-lane group g takes tokens
         // g, g + 4 of row rr.
@@ -788,12 +921,13 @@ template <int TM, bool EXN> static hipError_t launch_decode(const QeDecodeArgs &
         if ((e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_decode<TM, EXN>, NTH, L_TOTAL)) != hipSuccess) return e;
         if (per_cu < 1) return hipErrorInvalidConfiguration;
         // one workgroup per CU, 64..256 of them (a workgroup's D rows, <= 4 groups
-        // of 8, stay within the 32-row residual buffer)
+        // of 8, stay within the 32-row residual buffer); per_cu is 1 (LDS), so the
+        // grid is resident in full on an idle device
         grid = cus < 256 ? cus : 256;
         if (grid < DEC_MIN_GRID) return hipErrorInvalidConfiguration;
     }
     void *args[] = {(void *)&a};
-    return hipLaunchCooperativeKernel((const void *)k_decode<TM, EXN>, dim3(grid), dim3(NTH), args, L_TOTAL, st);
+    return hipLaunchKernel((const void *)k_decode<TM, EXN>, dim3(grid), dim3(NTH), args, L_TOTAL, st);
 }
 
 hipError_t qe_launch_decode(const QeDecodeArgs &a, hipStream_t st) {

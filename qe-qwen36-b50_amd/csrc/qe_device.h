@@ -197,6 +197,21 @@ QE_DEV unsigned f2ord(float v) {
 }
 QE_DEV float ord2f(unsigned o) { return __uint_as_float((o & 0x80000000u) ? (o & 0x7fffffffu) : ~o); }
 
+// Weights and shared gate of a selection: lane k < 8 holds the k-th selected
+// logit `mine` and its expert; sel0 is the largest.  w_k = exp(l_k - l_0) /
+// sum_j exp(l_j - l_0), the sum in k order; shg = sigmoid(logit 256).
+QE_DEV void topk_finish(float mine, int myid, float sel0, float lg_sh, int lane, int32_t *ids, float *wts, float *shg) {
+    const float ex = expf(mine - sel0);
+    float s = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ex), 0));
+#pragma unroll
+    for (int k = 1; k < QE_K_USED; ++k) s += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ex), k));
+    if (lane < QE_K_USED) {
+        ids[lane] = myid;
+        wts[lane] = ex / s;
+    }
+    if (lane == QE_K_USED) *shg = 1.f / (1.f + expf(-lg_sh));
+}
+
 // v[j] = logit of expert lane + 64 j; lg_sh = logit 256 (shared-expert gate).
 // Each round: one wave max of the values (as order-preserving u32, -0 folded
 // onto +0, so equal logits compare equal as in the reference), then one wave
@@ -230,15 +245,7 @@ QE_DEV int wave_topk_vals(const float v_in[4], float lg_sh, int lane, int32_t *i
 #pragma unroll
     for (int k = 1; k < QE_K_USED; ++k)
         if (lane == k) { mine = sel[k]; myid = id[k]; }
-    const float ex = expf(mine - sel[0]);
-    float s = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ex), 0));
-#pragma unroll
-    for (int k = 1; k < QE_K_USED; ++k) s += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ex), k));
-    if (lane < QE_K_USED) {
-        ids[lane] = myid;
-        wts[lane] = ex / s;
-    }
-    if (lane == QE_K_USED) *shg = 1.f / (1.f + expf(-lg_sh));
+    topk_finish(mine, myid, sel[0], lg_sh, lane, ids, wts, shg);
     return myid;
 }
 // One canonical normalisation of a 2048-vector by one wave.  Lane c owns the
