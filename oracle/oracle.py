@@ -56,6 +56,7 @@ def load():
         "orc_dot_nl4": (f32, [vp, i32, vp, vp]),
         "orc_dot_nl4_avx2": (f32, [vp, i32, vp, vp]),
         "orc_canon_dot": (f32, [vp, vp]),
+        "orc_canon_sumsq": (f32, [vp]),
         "orc_rmsnorm": (None, [vp, vp, i32, vp]),
         "orc_router": (None, [vp, vp, vp, i32, vp]),
         "orc_topk": (None, [vp, i32, vp, vp, vp]),
@@ -137,6 +138,10 @@ def dot_nl4(row, cols, xq, xs, avx2=False):
 
 def canon_dot(a, b):
     return load().orc_canon_dot(_p(np.ascontiguousarray(a, np.float32)), _p(np.ascontiguousarray(b, np.float32)))
+
+
+def canon_sumsq(x):
+    return load().orc_canon_sumsq(_p(np.ascontiguousarray(x, np.float32)))
 
 
 def rmsnorm(x, w=None):

@@ -16,9 +16,9 @@
 //   rmsnorm ............ engine/qe.cpp:159-168
 //   Q8 block dot ....... engine/qe.cpp:91-100 (shared expert, fp32 activations)
 // Two places define an order the reference leaves implementation-defined (its
-// GPU sub-group reductions): the router dot product and the RMSNorm sum of
-// squares use the canonical order of canon_dot() below, which the HIP kernels
-// reproduce exactly so that routing is bit-exact.
+// GPU sub-group reductions): the router dot product (canon_dot) and the RMSNorm
+// sum of squares (canon_sumsq) use canonical orders defined below, which the
+// HIP kernels reproduce exactly so that routing is bit-exact.
 //
 // Parity unpinned: nothing available here pins the reference's GPU kernel
 // outputs (Intel sub-group reduction order, icpx contraction, the XMX
@@ -177,7 +177,7 @@ ORC_API float orc_dot_nl4_avx2(const uint8_t *row, int cols, const int8_t *xq, c
 }
 
 // ---------------------------------------------------------------------------
-// canonical fp32 dot of length 2048 (router rows, RMSNorm sum of squares):
+// canonical fp32 dot of length 2048 (router rows):
 //   64 chunks of 32 contiguous elements, each an fma chain from 0 in index
 //   order; chunk sums combined by the pairwise tree (c, c+1), (c, c+2), ...,
 //   (c, c+32) -- the value an xor-butterfly over 64 lanes with offsets
@@ -196,11 +196,28 @@ static float canon_dot(const float *a, const float *b) {
 }
 ORC_API float orc_canon_dot(const float *a, const float *b) { return canon_dot(a, b); }
 
+// Canonical RMSNorm sum of squares: 256 groups of 8 contiguous elements, each
+// an fma chain from 0 in index order, combined by the pairwise tree over the
+// groups ((g0+g1)+(g2+g3))+... -- the order the decode kernel can assemble from
+// per-workgroup partials of its 8-row output groups.
+static float canon_sumsq(const float *x) {
+    float p[256];
+    for (int g = 0; g < 256; ++g) {
+        float acc = 0.f;
+        for (int i = 0; i < 8; ++i) acc = fmaf(x[g * 8 + i], x[g * 8 + i], acc);
+        p[g] = acc;
+    }
+    for (int s = 1; s < 256; s *= 2)
+        for (int j = 0; j < 256; j += 2 * s) p[j] = p[j] + p[j + s];
+    return p[0];
+}
+ORC_API float orc_canon_sumsq(const float *x) { return canon_sumsq(x); }
+
 // RMSNorm (qe.cpp:159-168): xn = x * (1/sqrt(ss/2048 + eps)) * w.
 ORC_API void orc_rmsnorm(const float *x, const float *w, int T, float *xn) {
     for (int t = 0; t < T; ++t) {
         const float *xr = x + (size_t)t * D;
-        const float ss = canon_dot(xr, xr);
+        const float ss = canon_sumsq(xr);
         const float inv = 1.0f / sqrtf(ss / (float)D + QE_RMS_EPS);
         for (int i = 0; i < D; ++i) xn[(size_t)t * D + i] = (xr[i] * inv) * (w ? w[i] : 1.0f);
     }

@@ -82,7 +82,8 @@ QE_DEV int xpos(int e) { return (e & 31) * 65 + (e >> 5); } // raw x element e o
 #define L_MISC (L_SHG + 8 * 4)                      // int [16]
 #define L_INV (L_MISC + 16 * 4)                     // f32 [8]          1 / rms of each token
 #define L_SD (L_INV + 8 * 4)                        // f32 [4][8][T]    shared-expert output of the D rows
-#define L_TK (L_SD + 4 * 8 * DEC_T * 4)            // T = 1 top-8: u64 [256] survivor order keys, int [256] their
+#define L_GX (L_SD + 4 * 8 * DEC_T * 4)            // f32 [T][8] the 8 output rows of a group, per token
+#define L_TK (L_GX + DEC_T * 8 * 4)            // T = 1 top-8: u64 [256] survivor order keys, int [256] their
                                                     //   experts, u32 [8] logit keys by rank, f32 logit 256
 #define L_TOTAL (L_TK + 256 * 8 + 256 * 4 + 8 * 4 + 16)
 static_assert(L_Y + 8 * 2 * DEC_T * 4 <= L_U_END, "D-stage LDS must fit in the union");
@@ -95,7 +96,8 @@ static_assert(L_TOTAL <= 160 * 1024, "LDS budget of one workgroup per CU");
 #define EX_HSH (EX_L + DEC_T * QE_ROUTER_ROWS)      // [T][512] f32 shared silu(g)*u
 #define EX_HQ (EX_HSH + DEC_T * QE_FF_SH)           // [T*8][16][9]: 8 x int8x4, 1 x f32 scale
 #define EX_HF (EX_HQ + DEC_T * 8 * 16 * 9)          // [8][512] f32 h (T = 1)
-#define EX_TOTAL (EX_HF + 8 * QE_FF_EXP)           // one replica
+#define EX_XS (EX_HF + 8 * QE_FF_EXP)               // 2 x [T][256] f32 sum-of-squares partial of each 8-row group of x
+#define EX_TOTAL (EX_XS + 2 * DEC_T * 256)          // one replica
 static_assert(REP * EX_TOTAL == QE_DECODE_EX_WORDS, "exchange size must match the allocation");
 static_assert(SYNC_EXIT < QE_DECODE_SYNC_WORDS, "sync words must match the allocation");
 
@@ -226,6 +228,8 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
         const unsigned tagIn = tagR - 2u;                              // x of this layer (li > 0)
         const uint64_t *src_x = EXr + EX_X + (size_t)((li - 1) & 1) * DEC_T * QE_D;
         uint64_t *dst_x = EX + EX_X + (size_t)(li & 1) * DEC_T * QE_D;
+        const uint64_t *src_xs = EXr + EX_XS + (size_t)((li - 1) & 1) * DEC_T * 256;
+        uint64_t *dst_xs = EX + EX_XS + (size_t)(li & 1) * DEC_T * 256;
         const uint8_t *arena = a.arena + (size_t)l * QE_LAYER_EXPERT_BYTES;
         const float *router = a.router + (size_t)l * QE_ROUTER_ROWS * QE_D;
         const float *bias = a.bias_on[l] ? a.bias + (size_t)l * QE_N_EXPERT : nullptr;
@@ -276,9 +280,16 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
                 __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)(pnorm + i * 64 + lane),
                                                  (__attribute__((address_space(3))) void *)(s_pn + i * 65), 4, 0, 0);
         }
-        if (li > 0 && tid < T * 256) { // x: one word per (8-row group, token) polled first; the
-            uint64_t w[1];               // rest of the workgroup polls its own words directly
-            read_tv<1>(src_x + (tid >> 8) * QE_D + (tid & 255) * 8 + 7, 0, tagIn, w, true, pc);
+        // x of a layer li > 0: wave t first polls token t's 256 group partials of
+        // the sum of squares (published with x, one word per 8-row group), which
+        // give 1/rms at once (canonical order: lane l holds groups 4l..4l+3); then
+        // the whole workgroup reads x, each thread polling its own words.
+        if (li > 0 && wv < T) {
+            const int t = wv;
+            uint64_t w[4];
+            read_tv<4>(src_xs + t * 256 + 4 * lane, 1, tagIn, w, true, pc);
+            const float ss = wave_sum_canon((tv_val(w[0]) + tv_val(w[1])) + (tv_val(w[2]) + tv_val(w[3])));
+            if (lane == 0) s_inv[t] = 1.0f / sqrtf(ss / (float)QE_D + QE_RMS_EPS);
         }
         // raw x of all tokens -> LDS (natural layout, token stride 2048; T*2048 is a multiple of 2 NTH)
         if (li == 0) {
@@ -293,10 +304,11 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
             }
         }
         __syncthreads();
-        // RMSNorm (wave_norm_chunk's arithmetic, spread over the workgroup): wave t
-        // takes the residual rows of token t and its sum of squares in the
-        // canonical order (lane = 32-element chunk); then threads scale, store in
-        // place and quantise 8 elements each (4 lanes per 32-block).
+        // RMSNorm: wave t takes the residual rows of token t and, for the first
+        // layer of the launch (x from the caller, no partials), its sum of squares
+        // in the canonical order (lane l holds elements [32l, 32l+32)); then
+        // threads scale, store in place and quantise 8 elements each (4 lanes per
+        // 32-block).
         if (wv < T) {
             const int t = wv;
             const float *xt = s_xn + t * DEC_XSTR;
@@ -304,18 +316,15 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
                 const int r = (blockIdx.x + (lane >> 3) * gridDim.x) * 8 + (lane & 7);
                 s_res[t * 32 + lane] = r < QE_D ? xt[xpos(r)] : 0.f;
             }
-            if (pnorm) {
-                float ss = 0.f;
+            if (li == 0 && pnorm) {
+                float c[32];
 #pragma unroll
-                for (int i = 0; i < 32; ++i) {
-                    const float x = xt[i * 65 + lane];
-                    ss = fmaf(x, x, ss);
-                }
-                ss = wave_sum_canon(ss);
+                for (int i = 0; i < 32; ++i) c[i] = xt[i * 65 + lane];
+                const float ss = wave_sum_canon(sumsq_lane32(c));
                 if (lane == 0) s_inv[t] = 1.0f / sqrtf(ss / (float)QE_D + QE_RMS_EPS);
             }
         }
-        __syncthreads();
+        if (li == 0) __syncthreads(); // later layers had 1/rms before the x read
         for (int w = tid; w < T * 256; w += NTH) { // 8 elements of token t per thread, 4 lanes per block
             const int t = w >> 8, e = 8 * (w & 255);
             float *xt = s_xn + t * DEC_XSTR;
@@ -848,6 +857,16 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
                 if (!last || EXN) { // the exit norm reads the last x like a next layer would
 #pragma unroll
                     for (int r = 0; r < REP; ++r) ST_A(dst_x + r * EX_TOTAL + o, pack_tv(out, tagD));
+                    // the group's partial of the next norm's sum of squares (an fma
+                    // chain over its 8 rows), gathered in LDS by the thread of row 0;
+                    // these threads are all in wave 0, whose LDS accesses are ordered
+                    float *s_gx = (float *)(lds + L_GX);
+                    s_gx[t * 8 + k] = out;
+                    if (k == 0) {
+                        const float g = sumsq_group8(s_gx + t * 8);
+#pragma unroll
+                        for (int r = 0; r < REP; ++r) ST_A(dst_xs + r * EX_TOTAL + t * 256 + rb / 8, pack_tv(g, tagD));
+                    }
                 }
             }
             __syncthreads(); // s_y is rewritten by the next row group
@@ -870,13 +889,10 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
         __syncthreads();
         if (threadIdx.x < 64) {
             const int lane = threadIdx.x;
-            float ss = 0.f;
+            float c[32];
 #pragma unroll
-            for (int i = 0; i < 32; ++i) {
-                const float x = s_xn[i * 65 + lane];
-                ss = fmaf(x, x, ss);
-            }
-            ss = wave_sum_canon(ss);
+            for (int i = 0; i < 32; ++i) c[i] = s_xn[i * 65 + lane];
+            const float ss = wave_sum_canon(sumsq_lane32(c));
             if (lane == 0) s_inv[0] = 1.0f / sqrtf(ss / (float)QE_D + QE_RMS_EPS);
         }
         __syncthreads();

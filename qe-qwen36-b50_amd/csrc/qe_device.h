@@ -248,14 +248,27 @@ QE_DEV int wave_topk_vals(const float v_in[4], float lg_sh, int lane, int32_t *i
     topk_finish(mine, myid, sel[0], lg_sh, lane, ids, wts, shg);
     return myid;
 }
+// Canonical RMSNorm sum of squares of a 2048-vector: 256 groups of 8
+// contiguous elements, each an fma chain from 0 in index order, combined by the
+// pairwise tree over the groups (adjacent pairs first).  A lane holding the 32
+// elements [32c, 32c+32) forms groups 4c..4c+3 and the first two tree levels;
+// wave_sum_canon over the 64 lanes is the rest of the tree.  (Groups of 8 are
+// what one decode workgroup produces, so its partial travels with its rows.)
+QE_DEV float sumsq_group8(const float *v) {
+    float g = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) g = fmaf(v[i], v[i], g);
+    return g;
+}
+QE_DEV float sumsq_lane32(const float v[32]) {
+    return (sumsq_group8(v) + sumsq_group8(v + 8)) + (sumsq_group8(v + 16) + sumsq_group8(v + 24));
+}
+
 // One canonical normalisation of a 2048-vector by one wave.  Lane c owns the
 // 32 contiguous elements [32c, 32c+32) in v[]; on return v holds xn.
 QE_DEV void wave_norm_chunk(float v[32], const float *post_norm, int lane) {
     if (!post_norm) return;
-    float ss = 0.f;
-#pragma unroll
-    for (int i = 0; i < 32; ++i) ss = fmaf(v[i], v[i], ss);
-    ss = wave_sum_canon(ss);
+    const float ss = wave_sum_canon(sumsq_lane32(v));
     const float inv = 1.0f / sqrtf(ss / (float)QE_D + QE_RMS_EPS);
     const float4 *wr = (const float4 *)(post_norm + lane * 32);
 #pragma unroll

@@ -93,7 +93,8 @@ hipError_t qe_launch_decode(const QeDecodeArgs &a, hipStream_t st);
 #define QE_DEC_REP 4 /* copies of every decode exchange buffer */
 #endif
 #define QE_DECODE_EX_WORDS \
-    (QE_DEC_REP * (2 * QE_SMALL_T * QE_D + QE_SMALL_T * QE_ROUTER_ROWS + QE_SMALL_T * QE_FF_SH + QE_SMALL_T * 8 * 16 * 9 + 8 * QE_FF_EXP))
+    (QE_DEC_REP * (2 * QE_SMALL_T * QE_D + QE_SMALL_T * QE_ROUTER_ROWS + QE_SMALL_T * QE_FF_SH + QE_SMALL_T * 8 * 16 * 9 + \
+                   8 * QE_FF_EXP + 2 * QE_SMALL_T * 256))
 #define QE_DECODE_SYNC_WORDS 64 /* launch epoch, exit counter */
 #define QE_DECODE_SPIN_CAP (1 << 22) /* poll reads (s_sleep 1 between) before an exchange wait gives up */
 

@@ -239,8 +239,9 @@ __global__ __launch_bounds__(256) void k_combine(QeCombineArgs a) {
 // (engine/qe.cpp:1280, rmsnorm_rows of the next layer's attn_norm, or :1295
 // out_norm after the last).  Workgroup per token: every thread combines 8
 // elements (coalesced as in k_combine) into LDS, 32-element chunks padded to 33
-// words; wave 0 forms the sum of squares (lane c = chunk c, an fma chain, then
-// the pairwise tree), and every thread scales its 8 elements.
+// words; wave 0 forms the sum of squares in the canonical order (lane c holds
+// elements [32c, 32c+32): sumsq_lane32, then the tree over the lanes), and
+// every thread scales its 8 elements.
 __global__ __launch_bounds__(256) void k_combine_norm(QeCombineArgs a) {
     __shared__ float s_x[64 * 33];
     __shared__ float s_inv;
@@ -276,10 +277,10 @@ __global__ __launch_bounds__(256) void k_combine_norm(QeCombineArgs a) {
     for (int i = 0; i < 8; ++i) s_x[(e0 >> 5) * 33 + (e0 & 31) + i] = v[i];
     __syncthreads();
     if (tid < 64) {
-        float ss = 0.f;
+        float c[32];
 #pragma unroll
-        for (int i = 0; i < 32; ++i) ss = fmaf(s_x[tid * 33 + i], s_x[tid * 33 + i], ss);
-        ss = wave_sum_canon(ss);
+        for (int i = 0; i < 32; ++i) c[i] = s_x[tid * 33 + i];
+        const float ss = wave_sum_canon(sumsq_lane32(c));
         if (tid == 0) s_inv = 1.0f / sqrtf(ss / (float)QE_D + QE_RMS_EPS);
     }
     __syncthreads();

@@ -159,6 +159,46 @@ def test_canon_dot_and_rmsnorm():
     assert np.allclose(O.rmsnorm(c, np.ones(2048, np.float32)), 3.0 / math.sqrt(9.0 + 1e-6), rtol=1e-7)
 
 
+def _sumsq_tree_f32(x):
+    """float32 emulation of the canonical sum of squares for inputs with one
+    non-zero element per group of 8 (the group's fma chain is then one rounded
+    square): the pairwise tree over the 256 groups, adjacent pairs first."""
+    p = (x.reshape(256, 8).astype(np.float32) ** 2).sum(axis=1, dtype=np.float32)
+    s = 1
+    while s < 256:
+        p[0::2 * s] = p[0::2 * s] + p[s::2 * s]
+        s *= 2
+    return p[0]
+
+
+def test_canon_sumsq_order():
+    rng = np.random.default_rng(11)
+    # small integers: every partial is exact, so any order gives the exact sum
+    xi = rng.integers(-20, 20, 2048).astype(np.float32)
+    assert O.canon_sumsq(xi) == float((xi.astype(np.int64) ** 2).sum())
+    # one non-zero per group, random magnitudes: bit-exact against the tree emulation
+    for trial in range(20):
+        x = np.zeros(2048, np.float32)
+        x[np.arange(256) * 8 + rng.integers(0, 8, 256)] = (rng.standard_normal(256) * 2.0 ** rng.integers(-6, 7, 256))
+        assert np.float32(O.canon_sumsq(x)) == _sumsq_tree_f32(x), trial
+    # adversarial: 2^24 in group 0 and 1 in every other group.  The tree loses only
+    # group 1 (2^24 + 1 rounds to 2^24) and gives 2^24 + 254; a sequential sum
+    # loses every 1, float64 keeps all
+    x = np.zeros(2048, np.float32)
+    x[0] = 4096.0
+    x[8::8] = 1.0
+    assert O.canon_sumsq(x) == 2.0 ** 24 + 254
+    seq = np.float32(0)
+    for v in (x.reshape(256, 8) ** 2).sum(axis=1, dtype=np.float32):
+        seq = np.float32(seq + v)
+    assert seq == 2.0 ** 24 and O.canon_sumsq(x) != seq
+    # the norm uses it: xn = x / sqrt(ss / 2048 + eps) * w, elementwise in fp32
+    w = (rng.random(2048) + 0.5).astype(np.float32)
+    xr = rng.standard_normal(2048).astype(np.float32)
+    inv = np.float32(1.0) / np.sqrt(np.float32(O.canon_sumsq(xr)) / np.float32(2048) + np.float32(1e-6), dtype=np.float32)
+    assert np.array_equal(O.rmsnorm(xr[None], w)[0], (xr * inv) * w)
+
+
 def _topk_ref(lg):
     """Closed form of engine/qe.cpp:1454-1483: order by (-value, e % 16, e // 16)."""
     e = np.arange(256)
