@@ -203,7 +203,7 @@ int qe_moe_synth_zipf_bias(uint64_t seed, int layer, double s, float *out);
 /* Decode poll timeouts.  The T <= 8 path synchronises workgroups through
  * bounded polls; a poll that gives up (a hung or starved peer) lets the
  * launch finish with invalid outputs and records it in a host-visible word.
- * The next call that looks reports it once as QE_ERR_STATE and clears it:
+ * The next call that looks reports each such launch once as QE_ERR_STATE:
  * every forward entry point checks at entry (without synchronising, so a
  * launch still running is reported by a later call), and qe_moe_get_routing,
  * qe_moe_get_logits and qe_moe_check after synchronising `stream`.  The

@@ -49,8 +49,9 @@ struct qe_moe_ctx {
     uint8_t *bias_on = nullptr;  // device copy of has_bias
     uint64_t *ex = nullptr;      // decode exchange words
     unsigned *sync = nullptr;    // decode launch epoch + exit counter
-    unsigned *err_host = nullptr; // pinned, host-mapped: 0, or 1 + epoch of a decode launch whose poll timed out
+    unsigned *err_host = nullptr; // pinned, host-mapped: 0, or 1 + epoch of the last decode launch whose poll timed out
     unsigned *err_dev = nullptr;  // the same word as the kernels address it
+    unsigned err_seen = 0;        // the value last reported
     int spin_cap = QE_DECODE_SPIN_CAP;
     float *pingpong[2] = {nullptr, nullptr};
     std::vector<void *> allocs;
@@ -93,10 +94,13 @@ static bool layer_ready(const qe_moe_ctx *c, int layer, std::string &missing) {
 }
 
 // A decode launch whose exchange poll timed out leaves 1 + its epoch in the
-// host-mapped error word.  Reported once, by the next call that looks.
+// host-mapped error word.  Every poll that gives up writes it, and such writes
+// to host memory can land after the host last looked, so the word is never
+// cleared: each value is reported once, by the next call that looks.
 static int take_decode_error(qe_moe_ctx *c, const char *where) {
-    const unsigned v = __atomic_exchange_n(c->err_host, 0u, __ATOMIC_ACQ_REL);
-    if (!v) return QE_OK;
+    const unsigned v = __atomic_load_n(c->err_host, __ATOMIC_ACQUIRE);
+    if (!v || v == c->err_seen) return QE_OK;
+    c->err_seen = v;
     return fail(QE_ERR_STATE, "%s: the decode launch of epoch %u timed out waiting for an exchange; its outputs are invalid",
                 where, v - 1u);
 }
