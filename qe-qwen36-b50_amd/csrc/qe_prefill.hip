@@ -397,12 +397,14 @@ __device__ __forceinline__ void expert_tile(const GemmTileArgs &a, const int4 it
 }
 
 // Every item runs NC = 2: gate/up over 8 row groups of 64 h rows, down over 16
-// of 128 output rows; workgroup b = (item b / RG, row group b % RG).  Big items
-// (33..64 pairs) run NT = 4, small ones NT = 2 or 1.
+// of 128 output rows.  Workgroup b runs on XCD b % 8 (round-robin dispatch);
+// all row groups of an item run on one XCD, so its activations come from HBM
+// once and from that XCD's L2 after: b = 8 (RG (item / 8) + yb) + item % 8.
+// Big items (33..64 pairs) run NT = 4, small ones NT = 2 or 1.
 template <bool GU> constexpr int expert_rg() { return GU ? QE_FF_EXP / 64 : QE_D / 128; }
 template <bool GU> QE_DEV void expert_unit(const GemmTileArgs &a, int b, ExpertSmem<GU> &sm) {
     constexpr int RG = expert_rg<GU>();
-    const int item = b / RG, yb = b % RG;
+    const int k = b >> 3, item = (k / RG) * 8 + (b & 7), yb = k % RG;
     if (item >= a.n_items[0]) return;
     const int4 it = a.items[item];
     static_assert(QE_MFMA_MC == 64, "items of up to four 16-row tiles");
@@ -413,10 +415,11 @@ template <bool GU> QE_DEV void expert_unit(const GemmTileArgs &a, int b, ExpertS
     else
         expert_tile<GU, 2, 1>(a, it, yb, sm);
 }
-// Upper bound of the workgroups over the items of np pairs: items of more than
-// QE_MFMA_MC / 2 pairs, plus at most one smaller item per expert.
+// Workgroups over the items of np pairs: an upper bound of the item count
+// (items of more than QE_MFMA_MC / 2 pairs, plus at most one smaller item per
+// expert) rounded up to whole groups of 8 items, times the row groups.
 template <bool GU> constexpr int expert_max_wg(int np) {
-    return expert_rg<GU>() * (np / (QE_MFMA_MC / 2 + 1) + 1 + QE_N_EXPERT);
+    return expert_rg<GU>() * (((np / (QE_MFMA_MC / 2 + 1) + 1 + QE_N_EXPERT) + 7) & ~7);
 }
 __global__ __launch_bounds__(256, 2) void k_expert_gu(GemmTileArgs a) {
     __shared__ ExpertSmem<true> sm;
@@ -899,7 +902,7 @@ hipError_t qe_launch_expert_mfma(const QeLayerPtrs &L, const QeScratch &S, int T
     k_expert_gu<<<expert_max_wg<true>(np), 256, 0, st>>>(g);
     g.aq = S.hqp; g.a_bytes = np * QE_FF_EXP; g.as = S.hs; g.a_row_div = 1; g.yp = S.yp;
     const int nsh = 8 * (QE_D / 128) * (((T + 63) / 64 + 7) / 8);
-    const int nr = (expert_max_wg<false>(np) + 7) & ~7; // shared tiles start on XCD 0
+    const int nr = expert_max_wg<false>(np); // a multiple of 8: shared tiles start on XCD 0
     k_expert_dn<<<nr + nsh, 256, 0, st>>>(g, nr, (const _Float16 *)S.shgu, T, L.sh_dn, S.sd);
     return hipGetLastError();
 }
