@@ -479,18 +479,31 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
                     }
                     S += (int)__popcll(bal);
                 }
-                for (int i0 = 0; i0 < S; i0 += 64) { // more than 64 survivors only with many equal logits
-                    const int i = i0 + lane;
-                    const uint64_t ki = s_sk[i < S ? i : 0];
-                    int r = 0, j = 0;
-                    for (; j + 4 <= S; j += 4) {
-                        const uint64_t k0 = s_sk[j], k1 = s_sk[j + 1], k2 = s_sk[j + 2], k3 = s_sk[j + 3];
-                        r += (int)(k0 > ki) + (int)(k1 > ki) + (int)(k2 > ki) + (int)(k3 > ki);
+                if (S <= 32) {
+                    // up to 32 survivors: one per lane, sorted in registers (no LDS round
+                    // trips); a key's low half holds 0xffff - tie key, so it names its expert
+                    const uint64_t ki = lane < S ? s_sk[lane] : 0ull; // real keys are never 0
+                    uint32_t khi = (uint32_t)(ki >> 32), klo = (uint32_t)ki;
+                    sort32_desc_u64(khi, klo, lane);
+                    if (lane < QE_K_USED) {
+                        const unsigned tk = 0xffffu - (klo & 0xffffu); // (e % 16) * 16 + e / 16
+                        s_items[lane] = make_int4((int)(((tk & 15u) << 4) | ((tk >> 4) & 15u)), lane, 1, 0);
+                        s_rkey[lane] = khi;
                     }
-                    for (; j < S; ++j) r += (int)(s_sk[j] > ki);
-                    if (i < S && r < QE_K_USED) {
-                        s_items[r] = make_int4(s_se[i] & (QE_N_EXPERT - 1), r, 1, 0);
-                        s_rkey[r] = (unsigned)(ki >> 32);
+                } else {
+                    for (int i0 = 0; i0 < S; i0 += 64) { // many equal logits: count the survivors ahead
+                        const int i = i0 + lane;
+                        const uint64_t ki = s_sk[i < S ? i : 0];
+                        int r = 0, j = 0;
+                        for (; j + 4 <= S; j += 4) {
+                            const uint64_t k0 = s_sk[j], k1 = s_sk[j + 1], k2 = s_sk[j + 2], k3 = s_sk[j + 3];
+                            r += (int)(k0 > ki) + (int)(k1 > ki) + (int)(k2 > ki) + (int)(k3 > ki);
+                        }
+                        for (; j < S; ++j) r += (int)(s_sk[j] > ki);
+                        if (i < S && r < QE_K_USED) {
+                            s_items[r] = make_int4(s_se[i] & (QE_N_EXPERT - 1), r, 1, 0);
+                            s_rkey[r] = (unsigned)(ki >> 32);
+                        }
                     }
                 }
                 if (lane < QE_K_USED) s_pairs[lane] = lane;

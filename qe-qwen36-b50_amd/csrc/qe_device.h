@@ -156,6 +156,51 @@ QE_DEV unsigned wave_max_u32(unsigned v) {
     return umax32(a, b);
 }
 QE_DEV unsigned umin32(unsigned a, unsigned b) { return a < b ? a : b; }
+// Bitonic sort of 32 lanes (each half of the wave on its own), descending by
+// the 64-bit key (hi, lo), every comparator pointing the same way: for blocks
+// k = 2, 4, .., 32, lane i meets its mirror i ^ (k - 1) in the block, then
+// i ^ j for j = k/4 .. 1, and the lower lane of each pair keeps the larger
+// key.  Partners come by DPP (quad_perm, row mirrors, row_ror:8 for xor 8,
+// row_shr/shl:4 for xor 4) and, for the 32-lane mirror, a 16-lane row swap.
+QE_DEV void cx64(uint32_t &hi, uint32_t &lo, uint32_t phi, uint32_t plo, bool lower) {
+    const uint64_t k = ((uint64_t)hi << 32) | lo, p = ((uint64_t)phi << 32) | plo;
+    if (lower == (p > k)) {
+        hi = phi;
+        lo = plo;
+    }
+}
+QE_DEV void sort32_desc_u64(uint32_t &hi, uint32_t &lo, int lane) {
+    auto xor1 = [&]() { cx64(hi, lo, dpp_u<QE_DPP_XOR1>(hi), dpp_u<QE_DPP_XOR1>(lo), !(lane & 1)); };
+    auto xor2 = [&]() { cx64(hi, lo, dpp_u<QE_DPP_XOR2>(hi), dpp_u<QE_DPP_XOR2>(lo), !(lane & 2)); };
+    auto xor4 = [&]() { // row_shr:4 (from lane i - 4) where bit 2 is set, row_shl:4 (from i + 4) where clear
+        const bool up = lane & 4;
+        const uint32_t rh = dpp_u<0x114>(hi), lh = dpp_u<0x104>(hi); // both, then a select:
+        const uint32_t rl = dpp_u<0x114>(lo), ll = dpp_u<0x104>(lo); // DPP does not run under a branch
+        cx64(hi, lo, up ? rh : lh, up ? rl : ll, !up);
+    };
+    xor1();                                                                           // k = 2
+    cx64(hi, lo, dpp_u<0x1B>(hi), dpp_u<0x1B>(lo), !(lane & 2));                      // k = 4: quad_perm [3,2,1,0]
+    xor1();
+    cx64(hi, lo, dpp_u<QE_DPP_HMIRROR>(hi), dpp_u<QE_DPP_HMIRROR>(lo), !(lane & 4));  // k = 8
+    xor2();
+    xor1();
+    cx64(hi, lo, dpp_u<QE_DPP_MIRROR>(hi), dpp_u<QE_DPP_MIRROR>(lo), !(lane & 8));    // k = 16
+    xor4();
+    xor2();
+    xor1();
+    {   // k = 32: the mirror in the other 16-lane row of the pair
+        unsigned ah, bh, al, bl;
+        rows16(dpp_u<QE_DPP_MIRROR>(hi), ah, bh);
+        rows16(dpp_u<QE_DPP_MIRROR>(lo), al, bl);
+        const bool r1 = lane & 16;
+        cx64(hi, lo, r1 ? ah : bh, r1 ? al : bl, !r1);
+    }
+    cx64(hi, lo, dpp_u<0x128>(hi), dpp_u<0x128>(lo), !(lane & 8));                  // row_ror:8 = xor 8
+    xor4();
+    xor2();
+    xor1();
+}
+
 QE_DEV unsigned wave_min_u32(unsigned v) {
     v = umin32(v, dpp_ub<QE_DPP_XOR1>(v));
     v = umin32(v, dpp_ub<QE_DPP_XOR2>(v));
