@@ -178,6 +178,34 @@ QE_DEV void unit_rows(const uint8_t *row, int c, int row_in_unit, const int4 it,
     }
 }
 
+// Chunk `lane` (elements 32 lane .. 32 lane + 31) of a token's x in LDS, every
+// read issued before any is used.  Left to itself the scheduler streams the
+// reads into an fma chain two at a time, each pair waiting for the last:
+// sixteen LDS round trips in series.
+QE_DEV void lds_chunk32(const float *xt, int lane, float (&c)[32]) {
+#pragma unroll
+    for (int i = 0; i < 32; ++i) c[i] = xt[i * 65 + lane];
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+// Q8_0 quantisation of 8 consecutive elements held by one lane, four lanes
+// (xor 1, 2 neighbours) per 32-block: block maximum, scale, int8 values; the
+// scale is stored where xs is not null (one lane of the four).
+QE_DEV void quant8_block4(const float (&v)[8], int8_t *xq, float *xs) {
+    float am = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) am = fmaxf(am, fabsf(v[i]));
+    am = fmaxf(am, dpp_f<QE_DPP_XOR1>(am));
+    am = fmaxf(am, dpp_f<QE_DPP_XOR2>(am));
+    float dq;
+    const float id = quant_scale_inv(am, dq);
+    unsigned q[2] = {0u, 0u};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) q[i >> 2] |= (unsigned)(uint8_t)quant_one(v[i], id) << (8 * (i & 3));
+    *(uint2 *)xq = make_uint2(q[0], q[1]);
+    if (xs) *xs = dq;
+}
+
 // TM = 1: the single-token kernel (B = 1 decode); TM = 8: any T <= 8.
 template <int TM, bool EXN>
 __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
@@ -304,57 +332,66 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
             }
         }
         __syncthreads();
-        // RMSNorm: wave t takes the residual rows of token t and, for the first
-        // layer of the launch (x from the caller, no partials), its sum of squares
-        // in the canonical order (lane l holds elements [32l, 32l+32)); then
-        // threads scale, store in place and quantise 8 elements each (4 lanes per
-        // 32-block).
-        if (wv < T) {
+        // First layer of the launch (x from the caller, no partials): wave t forms
+        // token t's sum of squares in the canonical order (lane l holds elements
+        // [32l, 32l+32)).
+        if (li == 0 && pnorm && wv < T) {
             const int t = wv;
             const float *xt = s_xn + t * DEC_XSTR;
-            if (a.residual && lane < 8 * d_iters) { // raw x of this workgroup's D rows
-                const int r = (blockIdx.x + (lane >> 3) * gridDim.x) * 8 + (lane & 7);
-                s_res[t * 32 + lane] = r < QE_D ? xt[xpos(r)] : 0.f;
-            }
-            if (li == 0 && pnorm) {
-                float c[32];
+            float c[32];
 #pragma unroll
-                for (int i = 0; i < 32; ++i) c[i] = xt[i * 65 + lane];
-                const float ss = wave_sum_canon(sumsq_lane32(c));
-                if (lane == 0) s_inv[t] = 1.0f / sqrtf(ss / (float)QE_D + QE_RMS_EPS);
-            }
+            for (int i = 0; i < 32; ++i) c[i] = xt[i * 65 + lane];
+            const float ss = wave_sum_canon(sumsq_lane32(c));
+            if (lane == 0) s_inv[t] = 1.0f / sqrtf(ss / (float)QE_D + QE_RMS_EPS);
         }
         if (li == 0) __syncthreads(); // later layers had 1/rms before the x read
-        for (int w = tid; w < T * 256; w += NTH) { // 8 elements of token t per thread, 4 lanes per block
-            const int t = w >> 8, e = 8 * (w & 255);
-            float *xt = s_xn + t * DEC_XSTR;
-            float v[8];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) v[i] = xt[xpos(e + i)];
-            if (pnorm) {
-                const float inv = s_inv[t];
-#pragma unroll
-                for (int i = 0; i < 8; ++i) v[i] = (v[i] * inv) * s_pn[(e >> 6) * 65 + (e & 63) + i];
+        // RMSNorm in place.  A thread that scales elements of this workgroup's D
+        // rows keeps their raw values first (the residual): no other thread
+        // writes them.
+        //   T = 1: one element per thread and step; the row tasks below need only
+        //          this fp32 xn, and its int8 quantisation for the routed units
+        //          is done after the barrier by wave 0, which has no row task.
+        //   T > 1: 8 elements per thread, scaled and quantised (4 lanes per
+        //          32-block) in one pass.
+        if constexpr (TM == 1) {
+            for (int e = tid; e < QE_D; e += NTH) {
+                float *px = s_xn + xpos(e);
+                float v = *px;
+                if (a.residual)
+                    for (int m = 0; m < d_iters; ++m)
+                        if ((e >> 3) == (int)blockIdx.x + m * (int)gridDim.x) s_res[m * 8 + (e & 7)] = v;
+                if (pnorm) {
+                    v = (v * s_inv[0]) * s_pn[(e >> 6) * 65 + (e & 63)];
+                    *px = v;
+                }
+                if (last && blockIdx.x == 0 && a.xn_out) a.xn_out[e] = v;
             }
-            float am = 0.f;
+        } else {
+            for (int w = tid; w < T * 256; w += NTH) {
+                const int t = w >> 8, e = 8 * (w & 255);
+                float *xt = s_xn + t * DEC_XSTR;
+                float v[8];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                xt[xpos(e + i)] = v[i];
-                am = fmaxf(am, fabsf(v[i]));
-            }
-            am = fmaxf(am, dpp_f<QE_DPP_XOR1>(am));
-            am = fmaxf(am, dpp_f<QE_DPP_XOR2>(am));
-            float dq;
-            const float id = quant_scale_inv(am, dq);
-            unsigned q[2] = {0u, 0u};
+                for (int i = 0; i < 8; ++i) v[i] = xt[xpos(e + i)];
+                if (a.residual)
+                    for (int m = 0; m < d_iters; ++m)
+                        if ((w & 255) == (int)blockIdx.x + m * (int)gridDim.x) {
 #pragma unroll
-            for (int i = 0; i < 8; ++i) q[i >> 2] |= (unsigned)(uint8_t)quant_one(v[i], id) << (8 * (i & 3));
-            *(uint2 *)(s_xq + t * QE_D + e) = make_uint2(q[0], q[1]);
-            if ((w & 3) == 0) s_xs[t * 64 + (e >> 5)] = dq;
-            if (last && blockIdx.x == 0 && a.xn_out) {
-                float4 *o = (float4 *)(a.xn_out + (size_t)t * QE_D + e);
-                o[0] = make_float4(v[0], v[1], v[2], v[3]);
-                o[1] = make_float4(v[4], v[5], v[6], v[7]);
+                            for (int i = 0; i < 8; ++i) s_res[t * 32 + m * 8 + i] = v[i];
+                        }
+                if (pnorm) {
+                    const float inv = s_inv[t];
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) v[i] = (v[i] * inv) * s_pn[(e >> 6) * 65 + (e & 63) + i];
+                }
+#pragma unroll
+                for (int i = 0; i < 8; ++i) xt[xpos(e + i)] = v[i];
+                quant8_block4(v, s_xq + t * QE_D + e, (w & 3) == 0 ? s_xs + t * 64 + (e >> 5) : nullptr);
+                if (last && blockIdx.x == 0 && a.xn_out) {
+                    float4 *o = (float4 *)(a.xn_out + (size_t)t * QE_D + e);
+                    o[0] = make_float4(v[0], v[1], v[2], v[3]);
+                    o[1] = make_float4(v[4], v[5], v[6], v[7]);
+                }
             }
         }
         __syncthreads();
@@ -371,9 +408,16 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
                     load32(router + (size_t)task * QE_D + lane * 32, wr);
                 }
                 for (int t = 0; t < T; ++t) {
+                    float xv[32];
+                    if constexpr (TM == 1) {
+                        lds_chunk32(s_xn, lane, xv);
+                    } else {
+#pragma unroll
+                        for (int i = 0; i < 32; ++i) xv[i] = s_xn[t * DEC_XSTR + i * 65 + lane];
+                    }
                     float acc = 0.f;
 #pragma unroll
-                    for (int i = 0; i < 32; ++i) acc = fmaf(wr[i], s_xn[t * DEC_XSTR + i * 65 + lane], acc);
+                    for (int i = 0; i < 32; ++i) acc = fmaf(wr[i], xv[i], acc);
                     acc = wave_sum_canon(acc);
                     if (lane < REP) ST_A(EX + lane * EX_TOTAL + EX_L + t * QE_ROUTER_ROWS + task, pack_tv(add_bias ? acc + b : acc, tagR));
                 }
@@ -397,21 +441,55 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
                     u1 = ((const uint4 *)(ru + lane * 32))[1];
                     usc = f16_bits_to_f32(((const uint16_t *)(ru + QE_D))[lane]);
                 }
-                float wg[32], wu[32];
-                unpack_i8x32(g0, g1, wg);
-                unpack_i8x32(u0, u1, wu);
-                for (int t = 0; t < T; ++t) {
-                    float ag = 0.f, au = 0.f;
-#pragma unroll
-                    for (int i = 0; i < 32; ++i) {
-                        const float xv = s_xn[t * DEC_XSTR + i * 65 + lane];
-                        ag = fmaf(wg[i], xv, ag);
-                        au = fmaf(wu[i], xv, au);
-                    }
+                auto publish = [&](int t, float ag, float au) {
                     ag = wave_sum_canon(ag * gsc);
                     au = wave_sum_canon(au * usc);
                     const float hv = silu_mul(ag, au);
                     if (lane < REP) ST_A(EX + lane * EX_TOTAL + EX_HSH + t * QE_FF_SH + j, pack_tv(hv, tagR));
+                };
+                if constexpr (TM == 1) {
+                    // one token: the weights stay packed (16 registers) and are
+                    // widened in the chain, so x can sit in 32 registers
+                    const uint32_t gd[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+                    const uint32_t ud[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+                    float xv[32];
+                    lds_chunk32(s_xn, lane, xv);
+                    float ag = 0.f, au = 0.f;
+#pragma unroll
+                    for (int i = 0; i < 32; ++i) {
+                        ag = fmaf((float)(int8_t)((gd[i >> 2] >> (8 * (i & 3))) & 0xff), xv[i], ag);
+                        au = fmaf((float)(int8_t)((ud[i >> 2] >> (8 * (i & 3))) & 0xff), xv[i], au);
+                    }
+                    publish(0, ag, au);
+                } else {
+                    float wg[32], wu[32];
+                    unpack_i8x32(g0, g1, wg);
+                    unpack_i8x32(u0, u1, wu);
+                    for (int t = 0; t < T; ++t) {
+                        float ag = 0.f, au = 0.f;
+#pragma unroll
+                        for (int i = 0; i < 32; ++i) {
+                            const float xv = s_xn[t * DEC_XSTR + i * 65 + lane];
+                            ag = fmaf(wg[i], xv, ag);
+                            au = fmaf(wu[i], xv, au);
+                        }
+                        publish(t, ag, au);
+                    }
+                }
+            }
+        }
+
+        if constexpr (TM == 1) {
+            // int8 quantisation of xn for the routed units (read in G, after the
+            // workgroup barrier that follows the top-8), by wave 0 before it polls
+            // the logits: 8 elements per lane and step, 4 lanes per 32-block
+            if (wv == 0) {
+                for (int w = lane; w < 256; w += 64) {
+                    const int e = 8 * w;
+                    float v[8];
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) v[i] = s_xn[xpos(e + i)];
+                    quant8_block4(v, s_xq + e, (w & 3) == 0 ? s_xs + (e >> 5) : nullptr);
                 }
             }
         }
