@@ -710,11 +710,14 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
                                      (size_t)((lane >= 32 ? QE_FF_EXP : 0) + j) * QE_GU_ROW_BYTES;
                 const uint4 q0 = *(const uint4 *)(row + c * 16), q1 = *(const uint4 *)(row + (c + 32) * 16);
                 const uint16_t r0 = ((const uint16_t *)(row + QE_D / 2))[c], r1 = ((const uint16_t *)(row + QE_D / 2))[c + 32];
-                const float d0 = f16_bits_to_f32(r0) * s_xs[c], d1 = f16_bits_to_f32(r1) * s_xs[c + 32];
-                float acc = d0 * (float)nl4_block_dot(nl4_decode_block<true>(q0), *(const uint4 *)(s_xq + c * 32),
-                                                      *(const uint4 *)(s_xq + c * 32 + 16));
-                acc = fmaf(d1, (float)nl4_block_dot(nl4_decode_block<true>(q1), *(const uint4 *)(s_xq + (c + 32) * 32),
-                                                    *(const uint4 *)(s_xq + (c + 32) * 32 + 16)), acc);
+                // x blocks c, c + 32 from LDS while the rows are on their way
+                const uint4 xa = *(const uint4 *)(s_xq + c * 32), xb = *(const uint4 *)(s_xq + c * 32 + 16);
+                const uint4 xc = *(const uint4 *)(s_xq + (c + 32) * 32), xd = *(const uint4 *)(s_xq + (c + 32) * 32 + 16);
+                const float xs0 = s_xs[c], xs1 = s_xs[c + 32];
+                __builtin_amdgcn_sched_barrier(0);
+                const float d0 = f16_bits_to_f32(r0) * xs0, d1 = f16_bits_to_f32(r1) * xs1;
+                float acc = d0 * (float)nl4_block_dot(nl4_decode_block<true>(q0), xa, xb);
+                acc = fmaf(d1, (float)nl4_block_dot(nl4_decode_block<true>(q1), xc, xd), acc);
                 acc = add_rows16(sum16(acc)); // lanes 0..31: g, lanes 32..63: u
                 const float g = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), 0));
                 const float u = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), 32));
