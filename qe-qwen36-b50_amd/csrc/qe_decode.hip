@@ -857,6 +857,14 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
                 }
             }
         }
+        // T = 1: the first prefetched down block is decoded to int8 now, while h
+        // is still on its way (about half the routed down's instructions)
+        nl4_blk wpre;
+        if constexpr (TM == 1) {
+            wpre = nl4_decode_block<true>(dpq[0]);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) asm volatile("" : "+v"(wpre.w[i]));
+        }
         if (mode16 && tid < 256) {
             uint64_t w[1];
             read_tv<1>(EXr + EX_HF + (tid >> 5) * QE_FF_EXP + (tid & 31) * 16 + 15, 0, tagG, w, true, pc);
@@ -905,15 +913,21 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
                 const int4 it = s_items[act ? u : half];
                 uint4 q;
                 uint16_t sraw;
-                if (m == 0 && k < 2) { // prefetched during G
-                    q = k == 0 ? dpq[0] : dpq[1];
-                    sraw = (uint16_t)(k == 0 ? dps[0] : dps[1]);
+                nl4_blk w;
+                if (TM == 1 && m == 0 && k == 0) { // prefetched during G, decoded before the h wait
+                    w = wpre;
+                    sraw = (uint16_t)dps[0];
                 } else {
-                    const uint8_t *drow = arena + (size_t)it.x * QE_EXPERT_BYTES + QE_EXPERT_DOWN_OFF + (size_t)r * QE_DN_ROW_BYTES;
-                    q = *(const uint4 *)(drow + l16 * 16);
-                    sraw = ((const uint16_t *)(drow + QE_FF_EXP / 2))[l16];
+                    if (m == 0 && k < 2) { // prefetched during G
+                        q = k == 0 ? dpq[0] : dpq[1];
+                        sraw = (uint16_t)(k == 0 ? dps[0] : dps[1]);
+                    } else {
+                        const uint8_t *drow = arena + (size_t)it.x * QE_EXPERT_BYTES + QE_EXPERT_DOWN_OFF + (size_t)r * QE_DN_ROW_BYTES;
+                        q = *(const uint4 *)(drow + l16 * 16);
+                        sraw = ((const uint16_t *)(drow + QE_FF_EXP / 2))[l16];
+                    }
+                    w = nl4_decode_block<TM == 1>(q); // T > 1: at the register limit
                 }
-                const nl4_blk w = nl4_decode_block<TM == 1>(q); // T > 1: at the register limit
                 const float sc = f16_bits_to_f32(sraw);
                 const int npair = act ? it.z : 0;
                 for (int j = 0; j < T; ++j) { // pairs of the item (<= T); wave-uniform trip count
