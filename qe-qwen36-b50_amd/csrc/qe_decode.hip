@@ -930,7 +930,9 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
                 }
                 const float sc = f16_bits_to_f32(sraw);
                 const int npair = act ? it.z : 0;
-                for (int j = 0; j < T; ++j) { // pairs of the item (<= T); wave-uniform trip count
+                // pairs of the item (<= T), as many rounds as the wave's largest item
+                // needs (wave-uniform: the sums below are cross-lane)
+                for (int j = 0; j < T && __any(j < npair); ++j) {
                     const bool pj = j < npair;
                     const int p = pj ? s_pairs[it.y + j] : 0, tp = p / QE_K_USED;
                     const int8_t *hq = s_hq + p * QE_FF_EXP + l16 * 32;
