@@ -322,13 +322,32 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
         // raw x of all tokens -> LDS (natural layout, token stride 2048; T*2048 is a multiple of 2 NTH)
         if (li == 0) {
             for (int i = tid; i < T * QE_D; i += NTH) s_xn[(i >> 11) * DEC_XSTR + xpos(i & 2047)] = a.x_in[i];
-        } else {
+        } else if (TM == 1 || T <= 2) {
             for (int i0 = 0; i0 < T * QE_D; i0 += 2 * NTH) {
                 uint64_t w[2];
                 read_tv<2>(src_x + i0 + tid, NTH, tagIn, w, true, pc);
                 const int e0 = i0 + tid, e1 = e0 + NTH;
                 s_xn[(e0 >> 11) * DEC_XSTR + xpos(e0 & 2047)] = tv_val(w[0]);
                 s_xn[(e1 >> 11) * DEC_XSTR + xpos(e1 & 2047)] = tv_val(w[1]);
+            }
+        } else {
+            // up to 16 words per thread: 8 polled together per round trip (T = 8: two)
+            for (int i0 = 0; i0 < T * QE_D; i0 += 8 * NTH) {
+                const int nw = (T * QE_D - i0) / NTH; // words left per thread: even (T * 2048 = 2 T NTH)
+                uint64_t w[8];
+                if (nw >= 8) {
+                    read_tv<8>(src_x + i0 + tid, NTH, tagIn, w, true, pc);
+                } else if (nw >= 4) {
+                    read_tv<4>(src_x + i0 + tid, NTH, tagIn, w, true, pc);
+                    if (nw == 6) read_tv<2>(src_x + i0 + 4 * NTH + tid, NTH, tagIn, w + 4, true, pc);
+                } else {
+                    read_tv<2>(src_x + i0 + tid, NTH, tagIn, w, true, pc);
+                }
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const int e = i0 + tid + i * NTH;
+                    if (i < nw) s_xn[(e >> 11) * DEC_XSTR + xpos(e & 2047)] = tv_val(w[i]);
+                }
             }
         }
         __syncthreads();

@@ -393,6 +393,45 @@ def test_cfg2_stack_40_layers(torch_cuda, T):
         m.close()
 
 
+@pytest.mark.parametrize("T", [2, 3, 4, 5, 6, 7])
+def test_short_stack_every_batch(torch_cuda, T):
+    """A 3-layer persistent launch at each batch size the T <= 8 kernel takes
+    between the two the 40-layer test covers: x crosses the exchange 2, 4, 6, 8,
+    10, 12 or 14 words per thread (polled in rounds of 8, then 4 and 2), and the
+    stack equals the layer-by-layer chain bit for bit, each layer matching the
+    oracle on the GPU's own input."""
+    torch = torch_cuda
+    n, seed = 3, SEED + 3300 + T
+    m = qe_moe.MoE(n_layers=n, t_max=8)
+    try:
+        for l in range(n):
+            m.synth_layer(l, seed, None)
+        x0 = O.gen_x(seed, 910 + T, T)
+        x_in = torch.from_numpy(x0).cuda()
+        x_out = torch.empty_like(x_in)
+        say(f"{n}-layer stack, T={T}")
+        m.forward_stack(0, n, x_in, x_out, T)
+        torch.cuda.synchronize()
+        m.check()
+        stack_gpu = x_out.cpu().numpy()
+        h = x0
+        for l in range(n):
+            L = O.SynthLayer(seed, l)
+            xi = torch.from_numpy(h).cuda()
+            yo = torch.empty_like(xi)
+            m.forward(l, xi, yo, T)
+            torch.cuda.synchronize()
+            g = m.routing(T)
+            g["logits"] = m.logits(T)
+            g["out"] = yo.cpu().numpy()
+            check_layer(L, g, h, norm=True)
+            h = g["out"]
+            del L
+        assert np.array_equal(stack_gpu.view(np.uint32), h.view(np.uint32)), "stack differs from the per-layer chain"
+    finally:
+        m.close()
+
+
 def test_errors_are_reported(ctx, torch_cuda):
     torch = torch_cuda
     x = torch.zeros(1, 2048, device="cuda")
