@@ -802,10 +802,10 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
         }
         d_prefetch(); // workgroups without a unit
         // ================= D: routed down + shared down + combine =================
-        // No counter: h is polled through its tags.  For T = 1 one word per unit
-        // (the row of its last wave) is polled first, then everything is read
-        // with the tags verified (a late word is re-read): polling all 4096 words
-        // from every workgroup would flood the memory system while it waits.
+        // No counter: h is polled through its tags, every thread its own words
+        // (T = 1: four, one round trip after they land).  A first poll of one
+        // word per unit by four waves, then the read of all, cost a second round
+        // trip on those waves: 2,023 against 2,092 tokens/s without it.
         // shared-expert activations of every token: written in R, long landed by now
         // (T = 1 read them in G)
         if constexpr (TM != 1) {
@@ -883,10 +883,6 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
             wpre = nl4_decode_block<true>(dpq[0]);
 #pragma unroll
             for (int i = 0; i < 8; ++i) asm volatile("" : "+v"(wpre.w[i]));
-        }
-        if (mode16 && tid < 256) {
-            uint64_t w[1];
-            read_tv<1>(EXr + EX_HF + (tid >> 5) * QE_FF_EXP + (tid & 31) * 16 + 15, 0, tagG, w, true, pc);
         }
         if (mode16) { // fp32 h of the 8 pairs -> LDS, then int8 per 32 rows
             // thread = 4 consecutive h of one pair, 8 lanes per 32-block (quant_x per block)
