@@ -85,7 +85,8 @@ QE_DEV int xpos(int e) { return (e & 31) * 65 + (e >> 5); } // raw x element e o
 #define L_GX (L_SD + 4 * 8 * DEC_T * 4)            // f32 [T][8] the 8 output rows of a group, per token
 #define L_TK (L_GX + DEC_T * 8 * 4)            // T = 1 top-8: u64 [256] survivor order keys, int [256] their
                                                     //   experts, u32 [8] logit keys by rank, f32 logit 256
-#define L_TOTAL (L_TK + 256 * 8 + 256 * 4 + 8 * 4 + 16)
+#define L_LG (L_TK + 256 * 8 + 256 * 4 + 8 * 4 + 16) // f32 [T][257] the last layer's logits (routing sink)
+#define L_TOTAL (L_LG + DEC_T * QE_ROUTER_ROWS * 4)
 static_assert(L_Y + 8 * 2 * DEC_T * 4 <= L_U_END, "D-stage LDS must fit in the union");
 static_assert(64 * 8 * 4 <= L_HQ - L_U, "G-stage LDS must fit in front of the D buffers");
 static_assert(L_TOTAL <= 160 * 1024, "LDS budget of one workgroup per CU");
@@ -319,9 +320,15 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
             const float ss = wave_sum_canon((tv_val(w[0]) + tv_val(w[1])) + (tv_val(w[2]) + tv_val(w[3])));
             if (lane == 0) s_inv[t] = 1.0f / sqrtf(ss / (float)QE_D + QE_RMS_EPS);
         }
-        // raw x of all tokens -> LDS (natural layout, token stride 2048; T*2048 is a multiple of 2 NTH)
+        // raw x of all tokens -> LDS (natural layout, token stride 2048; T*2048 = 2 T NTH)
         if (li == 0) {
-            for (int i = tid; i < T * QE_D; i += NTH) s_xn[(i >> 11) * DEC_XSTR + xpos(i & 2047)] = a.x_in[i];
+            if constexpr (TM == 1) { // both loads issued before either is stored
+                const float x0 = a.x_in[tid], x1 = a.x_in[tid + NTH];
+                s_xn[xpos(tid)] = x0;
+                s_xn[xpos(tid + NTH)] = x1;
+            } else {
+                for (int i = tid; i < T * QE_D; i += NTH) s_xn[(i >> 11) * DEC_XSTR + xpos(i & 2047)] = a.x_in[i];
+            }
         } else if (TM == 1 || T <= 2) {
             for (int i0 = 0; i0 < T * QE_D; i0 += 2 * NTH) {
                 uint64_t w[2];
@@ -549,10 +556,11 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
 #pragma unroll
                 for (int j = 0; j < 4; ++j) v[j] = f2ord(tv_val(w[j]) + 0.0f);
                 if (lane == 0) *s_lg256 = tv_val(w[4]);
-                if (last && blockIdx.x == 0) {
+                if (last && blockIdx.x == 0) { // kept for the routing sink
+                    float *s_lgs = (float *)(lds + L_LG);
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) a.logits[lane + 64 * j] = tv_val(w[j]);
-                    if (lane == 0) a.logits[QE_N_EXPERT] = tv_val(w[4]);
+                    for (int j = 0; j < 4; ++j) s_lgs[lane + 64 * j] = tv_val(w[j]);
+                    if (lane == 0) s_lgs[QE_N_EXPERT] = tv_val(w[4]);
                 }
                 unsigned g = umax32(umax32(v[0], v[1]), umax32(v[2], v[3]));
                 g = umax32(g, dpp_ub<QE_DPP_XOR1>(g));
@@ -614,10 +622,11 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
             float v[5];
 #pragma unroll
             for (int j = 0; j < 5; ++j) v[j] = tv_val(w[j]);
-            if (last && blockIdx.x == 0) {
+            if (last && blockIdx.x == 0) { // kept for the routing sink
+                float *s_lgs = (float *)(lds + L_LG) + t * QE_ROUTER_ROWS;
 #pragma unroll
-                for (int j = 0; j < 4; ++j) a.logits[t * QE_ROUTER_ROWS + lane + 64 * j] = v[j];
-                if (lane == 0) a.logits[t * QE_ROUTER_ROWS + QE_N_EXPERT] = v[4];
+                for (int j = 0; j < 4; ++j) s_lgs[lane + 64 * j] = v[j];
+                if (lane == 0) s_lgs[QE_N_EXPERT] = v[4];
             }
             wave_topk_vals(v, v[4], lane, s_ids + t * QE_K_USED, s_wts + t * QE_K_USED, s_shg + t);
         }
@@ -657,22 +666,6 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
             if (lane < np) s_pairs[lt + rank] = lane;
             if (first) s_items[item] = make_int4(e, lt, cnt, 0);
             if (lane == 0) s_misc[0] = __popcll(fm);
-            if (last && blockIdx.x == 0) {
-                if (lane < np) {
-                    a.pairs[lt + rank] = lane;
-                    a.ids[lane] = e;
-                    a.wts[lane] = s_wts[lane];
-                }
-                if (lane < T) a.shg[lane] = s_shg[lane];
-#pragma unroll
-                for (int k = 0; k < 4; ++k) { // per-expert offsets for the routing sink
-                    const int ee = lane * 4 + k;
-                    int o = 0;
-                    for (int q = 0; q < np; ++q) o += s_ids[q] < ee;
-                    a.off[ee] = o;
-                }
-                if (lane == 0) a.off[QE_N_EXPERT] = np;
-            }
         }
         if (TM != 1) __syncthreads();
         const int nitems = s_misc[0];
@@ -817,36 +810,12 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
         }
         __syncthreads();
         if (TM == 1 && wv == NWV - 1) {
-            // weights and shared gate of the selection (read after the h wait), and
-            // the routing sink of the last layer: ids by rank, pairs/off in expert
-            // order; by a wave the shared down rows leave idle
+            // weights and shared gate of the selection (read after the h wait), by a
+            // wave the shared down rows leave idle
             const unsigned *s_rkey = (const unsigned *)(lds + L_TK + 3072);
             const int myid = lane < QE_K_USED ? s_items[lane].x & (QE_N_EXPERT - 1) : 0;
             const float mine = ord2f(s_rkey[lane < QE_K_USED ? lane : 0]), sel0 = ord2f(s_rkey[0]);
             topk_finish(mine, myid, sel0, *(const float *)(lds + L_TK + 3104), lane, s_ids, s_wts, s_shg);
-            if (last && blockIdx.x == 0) {
-                int id8[QE_K_USED], rank = 0;
-#pragma unroll
-                for (int jj = 0; jj < QE_K_USED; ++jj) {
-                    id8[jj] = __builtin_amdgcn_readlane(myid, jj);
-                    rank += id8[jj] < myid || (id8[jj] == myid && jj < lane);
-                }
-                if (lane < QE_K_USED) {
-                    a.pairs[rank] = lane;
-                    a.ids[lane] = myid;
-                    a.wts[lane] = s_wts[lane];
-                }
-                if (lane == 0) a.shg[0] = s_shg[0];
-#pragma unroll
-                for (int k = 0; k < 4; ++k) { // per-expert offsets
-                    const int ee = lane * 4 + k;
-                    int o = 0;
-#pragma unroll
-                    for (int jj = 0; jj < QE_K_USED; ++jj) o += id8[jj] < ee;
-                    a.off[ee] = o;
-                }
-                if (lane == 0) a.off[QE_N_EXPERT] = QE_K_USED;
-            }
         }
         // The shared down rows of every D row group run first, while the routed
         // h is still on its way: wave (rr, half 0), 16-lane group g takes tokens
@@ -997,6 +966,48 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
             __syncthreads(); // s_y is rewritten by the next row group
         }
         __syncthreads(); // the LDS union is rewritten by the next layer's R stage
+    }
+
+    // Routing sink of the last layer, written once at the end by workgroup 0, off
+    // the layers' critical path, from what LDS still holds: the logits (kept in
+    // G), ids / weights / shared gates (ids in rank order per token), pairs and
+    // per-expert offsets in expert order (a stable counting sort: the slot of
+    // pair p is the number of pairs with a smaller expert plus the earlier pairs
+    // with the same one; T > 1 has it in s_pairs and the items, in expert order).
+    if (blockIdx.x == 0) {
+        const float *s_lgs = (const float *)(lds + L_LG);
+        for (int i = threadIdx.x; i < T * QE_ROUTER_ROWS; i += NTH) a.logits[i] = s_lgs[i];
+        if ((int)threadIdx.x < np) {
+            const int p = threadIdx.x;
+            a.ids[p] = s_ids[p];
+            a.wts[p] = s_wts[p];
+            if constexpr (TM == 1) {
+                const int e = s_ids[p];
+                int slot = 0;
+#pragma unroll
+                for (int q = 0; q < QE_K_USED; ++q) slot += s_ids[q] < e || (s_ids[q] == e && q < p);
+                a.pairs[slot] = p;
+            } else {
+                a.pairs[p] = s_pairs[p]; // slot p
+            }
+        }
+        if ((int)threadIdx.x < T) a.shg[threadIdx.x] = s_shg[threadIdx.x];
+        if (threadIdx.x <= QE_N_EXPERT) {
+            const int e = threadIdx.x;
+            int o = 0;
+            if constexpr (TM == 1) {
+#pragma unroll
+                for (int q = 0; q < QE_K_USED; ++q) o += s_ids[q] < e;
+            } else { // first item (expert order) with an expert >= e: its first slot
+                int lo = 0, hi = s_misc[0];
+                while (lo < hi) {
+                    const int mid = (lo + hi) >> 1;
+                    if (s_items[mid].x < e) lo = mid + 1; else hi = mid;
+                }
+                o = lo < s_misc[0] ? s_items[lo].y : np;
+            }
+            a.off[e] = o;
+        }
     }
 
     // Exit norm (the next block's input norm, engine/qe.cpp:2243 / :2574):
