@@ -83,8 +83,9 @@ QE_DEV int xpos(int e) { return (e & 31) * 65 + (e >> 5); } // raw x element e o
 #define L_INV (L_MISC + 16 * 4)                     // f32 [8]          1 / rms of each token
 #define L_SD (L_INV + 8 * 4)                        // f32 [4][8][T]    shared-expert output of the D rows
 #define L_GX (L_SD + 4 * 8 * DEC_T * 4)            // f32 [T][8] the 8 output rows of a group, per token
-#define L_TK (L_GX + DEC_T * 8 * 4)            // T = 1 top-8: u64 [256] survivor order keys, int [256] their
-                                                    //   experts, u32 [8] logit keys by rank, f32 logit 256
+#define L_TK (L_GX + DEC_T * 8 * 4)            // top-8 scratch: T = 1: u64 [256] survivor order keys, int [256] their
+                                                    //   experts, u32 [8] logit keys by rank, f32 logit 256;
+                                                    //   T > 1: u64 [8][32] survivor keys per token
 #define L_LG (L_TK + 256 * 8 + 256 * 4 + 8 * 4 + 16) // f32 [T][257] the last layer's logits (routing sink)
 #define L_TOTAL (L_LG + DEC_T * QE_ROUTER_ROWS * 4)
 static_assert(L_Y + 8 * 2 * DEC_T * 4 <= L_U_END, "D-stage LDS must fit in the union");
@@ -326,8 +327,18 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
                 const float x0 = a.x_in[tid], x1 = a.x_in[tid + NTH];
                 s_xn[xpos(tid)] = x0;
                 s_xn[xpos(tid + NTH)] = x1;
-            } else {
-                for (int i = tid; i < T * QE_D; i += NTH) s_xn[(i >> 11) * DEC_XSTR + xpos(i & 2047)] = a.x_in[i];
+            } else { // loads issued four at a time before their stores
+                for (int k0 = 0; k0 < 2 * T; k0 += 4) {
+                    float xv[4];
+#pragma unroll
+                    for (int k = 0; k < 4; ++k)
+                        if (k0 + k < 2 * T) xv[k] = a.x_in[tid + (k0 + k) * NTH];
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        const int i = tid + (k0 + k) * NTH;
+                        if (k0 + k < 2 * T) s_xn[(i >> 11) * DEC_XSTR + xpos(i & 2047)] = xv[k];
+                    }
+                }
             }
         } else if (TM == 1 || T <= 2) {
             for (int i0 = 0; i0 < T * QE_D; i0 += 2 * NTH) {
@@ -616,9 +627,22 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
             }
         } else if (wv < T) {
             const int t = wv;
-            uint64_t w[5];
-            read_tv<4>(EXr + EX_L + t * QE_ROUTER_ROWS + lane, 64, tagR, w, true, pc);
-            read_tv<1>(EXr + EX_L + t * QE_ROUTER_ROWS + QE_N_EXPERT, 0, tagR, w + 4, true, pc);
+            uint64_t w[5]; // the lane's four logits and (lane 0) logit 256, one poll loop
+            const uint64_t *src = EXr + EX_L + t * QE_ROUTER_ROWS;
+            for (int spins = 0;; ++spins) {
+                unsigned bad = 0;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    w[j] = LD_A((uint64_t *)src + lane + 64 * j);
+                    bad |= (unsigned)(w[j] >> 32) ^ tagR;
+                }
+                w[4] = lane == 0 ? LD_A((uint64_t *)src + QE_N_EXPERT) : ((uint64_t)tagR << 32);
+                bad |= (unsigned)(w[4] >> 32) ^ tagR;
+                if (__all(bad == 0)) break;
+                if (spins + 1 >= pc.cap) { poll_timeout(pc); break; }
+                __builtin_amdgcn_s_sleep(1);
+            }
+            w[4] = __builtin_amdgcn_readfirstlane((unsigned)w[4]); // logit 256 to every lane
             float v[5];
 #pragma unroll
             for (int j = 0; j < 5; ++j) v[j] = tv_val(w[j]);
@@ -628,7 +652,8 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
                 for (int j = 0; j < 4; ++j) s_lgs[lane + 64 * j] = v[j];
                 if (lane == 0) s_lgs[QE_N_EXPERT] = v[4];
             }
-            wave_topk_vals(v, v[4], lane, s_ids + t * QE_K_USED, s_wts + t * QE_K_USED, s_shg + t);
+            wave_topk_sorted(v, v[4], lane, (uint64_t *)(lds + L_TK) + 32 * t, s_ids + t * QE_K_USED, s_wts + t * QE_K_USED,
+                             s_shg + t);
         }
         __syncthreads();
         if (TM != 1 && wv == 0) {

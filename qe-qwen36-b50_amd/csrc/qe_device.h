@@ -293,6 +293,52 @@ QE_DEV int wave_topk_vals(const float v_in[4], float lg_sh, int lane, int32_t *i
     topk_finish(mine, myid, sel[0], lg_sh, lane, ids, wts, shg);
     return myid;
 }
+
+// The same selection, usually in fewer steps: each lane's maximum over its
+// four, then over groups of 8 lanes, gives eight maxima of distinct experts;
+// the smallest of them bounds the 8th largest logit from below, so the experts
+// at or above it (about 18 of 256) hold the top 8.  Up to 32 of them go one per
+// lane through `sk` (32 words of LDS) as 64-bit keys {ordered value, 0xffff -
+// tie key} and are sorted in registers; lanes 0..7 then hold the selection in
+// the reference's order.  More survivors (many equal logits) take the rounds
+// of wave_topk_vals.
+QE_DEV void wave_topk_sorted(const float v_in[4], float lg_sh, int lane, uint64_t *sk, int32_t *ids, float *wts,
+                             float *shg) {
+    unsigned v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = f2ord(v_in[j] + 0.0f);
+    unsigned g = umax32(umax32(v[0], v[1]), umax32(v[2], v[3]));
+    g = umax32(g, dpp_ub<QE_DPP_XOR1>(g));
+    g = umax32(g, dpp_ub<QE_DPP_XOR2>(g));
+    g = umax32(g, dpp_ub<QE_DPP_HMIRROR>(g)); // maximum of 32 experts (8 lanes)
+    g = umin32(g, dpp_ub<QE_DPP_MIRROR>(g));
+    unsigned ra, rb;
+    rows16(g, ra, rb);
+    g = umin32(ra, rb);
+    rows32(g, ra, rb);
+    g = umin32(ra, rb); // the smallest of the eight
+    int S = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const bool sv = v[j] >= g;
+        const unsigned long long bal = __ballot(sv);
+        const int pos = S + (int)__builtin_amdgcn_mbcnt_hi((unsigned)(bal >> 32), __builtin_amdgcn_mbcnt_lo((unsigned)bal, 0u));
+        const int e = lane + 64 * j;
+        if (sv && pos < 32) sk[pos] = ((uint64_t)v[j] << 32) | (0xffffu - (unsigned)((e & 15) * 16 + (e >> 4)));
+        S += (int)__popcll(bal);
+    }
+    if (S > 32) {
+        wave_topk_vals(v_in, lg_sh, lane, ids, wts, shg);
+        return;
+    }
+    const uint64_t ki = lane < S ? sk[lane] : 0ull; // real keys are never 0
+    uint32_t khi = (uint32_t)(ki >> 32), klo = (uint32_t)ki;
+    sort32_desc_u64(khi, klo, lane);
+    const unsigned tk = 0xffffu - (klo & 0xffffu); // (e % 16) * 16 + e / 16
+    const int myid = (int)(((tk & 15u) << 4) | ((tk >> 4) & 15u));
+    const float sel0 = ord2f((unsigned)__builtin_amdgcn_readfirstlane(khi));
+    topk_finish(ord2f(khi), myid, sel0, lg_sh, lane, ids, wts, shg);
+}
 // Canonical RMSNorm sum of squares of a 2048-vector: 256 groups of 8
 // contiguous elements, each an fma chain from 0 in index order, combined by the
 // pairwise tree over the groups (adjacent pairs first).  A lane holding the 32
