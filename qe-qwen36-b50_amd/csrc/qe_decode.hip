@@ -87,7 +87,8 @@ QE_DEV int xpos(int e) { return (e & 31) * 65 + (e >> 5); } // raw x element e o
                                                     //   experts, u32 [8] logit keys by rank, f32 logit 256;
                                                     //   T > 1: u64 [8][32] survivor keys per token
 #define L_LG (L_TK + 256 * 8 + 256 * 4 + 8 * 4 + 16) // f32 [T][257] the last layer's logits (routing sink)
-#define L_TOTAL (L_LG + DEC_T * QE_ROUTER_ROWS * 4)
+#define L_IORD (L_LG + DEC_T * QE_ROUTER_ROWS * 4)   // int [64] T > 1: items in unit deal order
+#define L_TOTAL (L_IORD + 64 * 4)
 static_assert(L_Y + 8 * 2 * DEC_T * 4 <= L_U_END, "D-stage LDS must fit in the union");
 static_assert(64 * 8 * 4 <= L_HQ - L_U, "G-stage LDS must fit in front of the D buffers");
 static_assert(L_TOTAL <= 160 * 1024, "LDS budget of one workgroup per CU");
@@ -690,6 +691,22 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
             }
             if (lane < np) s_pairs[lt + rank] = lane;
             if (first) s_items[item] = make_int4(e, lt, cnt, 0);
+            // the order units are dealt in: items with more pairs first (their
+            // units cost more), so that a workgroup's second unit is a light one;
+            // the same ballot walk over the 4-bit key 15 - cnt
+            {
+                const int ck = 15 - cnt;
+                unsigned long long ceq = fm;
+                int clt = 0;
+#pragma unroll
+                for (int bit = 3; bit >= 0; --bit) {
+                    const int my = (ck >> bit) & 1;
+                    const unsigned long long ones = __ballot(first && my);
+                    if (my) clt += __popcll(ceq & ~ones);
+                    ceq &= my ? ones : ~ones;
+                }
+                if (first) ((int *)(lds + L_IORD))[clt + __popcll(ceq & below)] = item;
+            }
             if (lane == 0) s_misc[0] = __popcll(fm);
         }
         if (TM != 1) __syncthreads();
@@ -777,7 +794,7 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
             }
         } else
         for (int unit = blockIdx.x; unit < nunits; unit += gridDim.x) {
-            const int4 it = s_items[unit / upi];
+            const int4 it = s_items[((const int *)(lds + L_IORD))[unit / upi]];
             const int j0 = (unit % upi) * JU;
             const bool up = wv >= 8;
             const uint8_t *base = arena + (size_t)it.x * QE_EXPERT_BYTES + (size_t)(up ? QE_FF_EXP : 0) * QE_GU_ROW_BYTES;
