@@ -16,9 +16,12 @@
 // ===========================================================================
 // large T kernels
 // ===========================================================================
-// wave per token: xn, xq, xs
+// wave per token: xn, xq, xs, and router row 256 (the shared-expert gate) as a
+// canonical wave dot while the token's xn sits in registers (lane l holds
+// elements [32l, 32l+32)), so k_topk need not read xn again
 __global__ __launch_bounds__(256) void k_normq(const float *x, int T, const float *post_norm, float *xn, int8_t *xqp,
-                                               float *xs, _Float16 *xhl, int32_t *chunk_hist, int nch) {
+                                               float *xs, _Float16 *xhl, int32_t *chunk_hist, int nch, const float *W,
+                                               float *logits) {
     // the workgroup's four rows move through LDS: coalesced float4 loads and
     // stores of the rows, lane c of wave w working on elements [32c, 32c+32) of
     // row w (chunks padded to 33 words: conflict-free both ways)
@@ -53,6 +56,20 @@ __global__ __launch_bounds__(256) void k_normq(const float *x, int T, const floa
         }
     }
     if (t >= T) return;
+    {
+        const float4 *w4 = (const float4 *)(W + (size_t)QE_N_EXPERT * QE_D + lane * 32);
+        float acc = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float4 w = w4[i];
+            acc = fmaf(v[4 * i], w.x, acc);
+            acc = fmaf(v[4 * i + 1], w.y, acc);
+            acc = fmaf(v[4 * i + 2], w.z, acc);
+            acc = fmaf(v[4 * i + 3], w.w, acc);
+        }
+        const float lg = wave_sum_canon(acc);
+        if (lane == 0) logits[(size_t)t * QE_ROUTER_ROWS + QE_N_EXPERT] = lg;
+    }
     store_hilo_block(v, (uint8_t *)xhl, QE_D, t, lane);
     lane_quant_store_opnd(v, xqp + (size_t)t * QE_D, lane, xs + (size_t)t * (QE_D / 32) + lane);
 }
@@ -60,13 +77,12 @@ __global__ __launch_bounds__(256) void k_normq(const float *x, int T, const floa
 static_assert(RT_SPLIT == 8, "k_topk merges eight router partials");
 
 // Wave per token, 4 tokens per workgroup: logits (router partials merged +
-// bias; row 256 as a canonical wave dot), then top-8, weights and the shared
-// gate (engine/qe.cpp:1454-1483).  The workgroup then adds its 32 expert ids
+// bias; row 256 came from k_normq), then top-8, weights and the shared gate
+// (engine/qe.cpp:1454-1483).  The workgroup then adds its 32 expert ids
 // to the dispatch histogram of its 1024-pair chunk (zeroed by k_normq), one
 // global add per distinct expert.
-__global__ __launch_bounds__(256) void k_topk(const float *part, const float *xn, const float *W, const float *bias,
-                                              int T, float *logits, int32_t *ids, float *wts, float *shg,
-                                              int32_t *chunk_hist) {
+__global__ __launch_bounds__(256) void k_topk(const float *part, const float *bias, int T, float *logits, int32_t *ids,
+                                              float *wts, float *shg, int32_t *chunk_hist) {
     __shared__ int s_h[QE_N_EXPERT];
     const int lane = threadIdx.x & 63, t = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (threadIdx.x < QE_N_EXPERT) s_h[threadIdx.x] = 0;
@@ -86,20 +102,7 @@ __global__ __launch_bounds__(256) void k_topk(const float *part, const float *xn
         v[j] = x;
         logits[(size_t)t * QE_ROUTER_ROWS + e] = x;
     }
-    float xv[32];
-    load32(xn + (size_t)t * QE_D + lane * 32, xv);
-    const float4 *w4 = (const float4 *)(W + (size_t)QE_N_EXPERT * QE_D + lane * 32);
-    float acc = 0.f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const float4 w = w4[i];
-        acc = fmaf(xv[4 * i], w.x, acc);
-        acc = fmaf(xv[4 * i + 1], w.y, acc);
-        acc = fmaf(xv[4 * i + 2], w.z, acc);
-        acc = fmaf(xv[4 * i + 3], w.w, acc);
-    }
-    const float lg = wave_sum_canon(acc);
-    if (lane == 0) logits[(size_t)t * QE_ROUTER_ROWS + QE_N_EXPERT] = lg;
+    const float lg = logits[(size_t)t * QE_ROUTER_ROWS + QE_N_EXPERT];
     const int e = wave_topk_vals(v, lg, lane, ids + t * QE_K_USED, wts + t * QE_K_USED, shg + t);
     if (lane < QE_K_USED) atomicAdd(&s_h[e], 1);
     }
@@ -330,7 +333,7 @@ hipError_t qe_launch_layer(const QeLayerPtrs &L, const QeScratch &S, const float
     {
         QE_PROF(QP_NORMQ);
         k_normq<<<(T + 3) / 4, 256, 0, st>>>(xin, T, pn, S.xn, S.xqp, S.xs, S.xhl, S.chunk_hist,
-                                              (T * QE_K_USED + 1023) / 1024);
+                                              (T * QE_K_USED + 1023) / 1024, L.router, S.logits);
     }
     {
         QE_PROF(QP_ROUTER);
@@ -339,8 +342,7 @@ hipError_t qe_launch_layer(const QeLayerPtrs &L, const QeScratch &S, const float
     }
     {
         QE_PROF(QP_TOPK);
-        k_topk<<<(T + 3) / 4, 256, 0, st>>>(S.rpart, S.xn, L.router, L.bias, T, S.logits, S.ids, S.wts, S.shg,
-                                             S.chunk_hist);
+        k_topk<<<(T + 3) / 4, 256, 0, st>>>(S.rpart, L.bias, T, S.logits, S.ids, S.wts, S.shg, S.chunk_hist);
     }
     {
         QE_PROF(QP_DISPATCH); // the histogram came with k_topk
