@@ -481,7 +481,7 @@ QE_DEV float half_of(const qe_u32x4 s[2], int b) { // fp16 scale b of 16 packed 
 // z computes the 8-chunk subtree [8z, 8z+8) exactly, and k_topk forms the top
 // three levels ((s0 + s1) + (s2 + s3)) + ((s4 + s5) + (s6 + s7)) -- bit-identical
 // to the unsplit order.  Row 256 (the shared-expert gate) is one canonical wave
-// dot per token in k_topk.  Tile 64 tokens x 64 rows, 256 threads, 4 x 4 outputs
+// dot per token in k_normq.  Tile 64 tokens x 64 rows, 256 threads, 4 x 4 outputs
 // per thread; chunks are double-buffered in LDS, k-major, the next one loaded
 // into registers while the current one is multiplied.  The transposing stores
 // XOR the column with the k group ((k / 8) % 4 * 16), so the four k groups a
