@@ -457,6 +457,8 @@ QE_DEV qe_u32x4 sh_ld(__amdgpu_buffer_rsrc_t r, uint32_t off) { return __builtin
 
 // one 32-block: acc += dw * (A_hi + A_lo) . B, A = a[0..3] (hi 0..7, hi 8..15, lo 0..7, lo 8..15)
 QE_DEV void sh_block(const qe_u32x4 a[4], qe_u32x4 w, float dw, qe_float16v &acc) {
+    // dw widened here, once: folded into each fma it becomes a half-rate v_fma_mix_f32
+    asm volatile("" : "+v"(dw));
     const qe_half8 b0 = i8x8_to_half8(w.x, w.y), b1 = i8x8_to_half8(w.z, w.w);
     qe_float16v p = {};
     p = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(qe_half8, a[0]), b0, p, 0, 0, 0);
