@@ -65,23 +65,28 @@ def test_decode_epoch_wrap(torch_cuda):
 
 
 def test_decode_poll_timeout_is_reported(torch_cuda):
-    # A poll cap of one read makes exchange waits give up (the producers cannot
-    # be that fast); the kernel still runs to its end, and the next call reports it.
+    # A poll cap of one read makes exchange waits give up; the kernel still runs
+    # to its end, and the next call reports it.  The forcing launch is a two-layer
+    # stack at T = 8: the second layer's x is polled by each workgroup as soon as
+    # it has published its own rows of the first layer's, microseconds before the
+    # slowest workgroup publishes its rows, so a first read misses.  (A single
+    # layer at T = 1 can find every word in place at the first read.)
     torch = torch_cuda
-    m = qe_moe.MoE(n_layers=1, t_max=8)
+    m = qe_moe.MoE(n_layers=2, t_max=8)
     try:
         L = O.SynthLayer(SEED, 0)
-        m.synth_layer(0, SEED, None)
+        for l in range(2):
+            m.synth_layer(l, SEED, None)
         x = O.gen_x(SEED, 3, 1)
         xd = torch.from_numpy(x).cuda()
         y = torch.empty_like(xd)
+        x8 = torch.from_numpy(O.gen_x(SEED, 4, 8)).cuda()
+        y8 = torch.empty_like(x8)
         m.debug_set_spin_cap(1)
-        say("poll timeout: forced by a one-read cap")
-        # every workgroup polls the logits of all router rows right after its own
-        # rows; with one read some poll misses (up to 5 launches allowed for that)
+        say("poll timeout: forced by a one-read cap, 2-layer stack at T=8")
         err = None
         for _ in range(5):
-            m.forward_normed(0, xd, y, 1)  # launches; its own timeout is not known yet
+            m.forward_stack(0, 2, x8, y8, 8)  # launches; its own timeout is not known yet
             try:
                 m.check()
             except qe_moe.QeError as ex:
@@ -90,9 +95,9 @@ def test_decode_poll_timeout_is_reported(torch_cuda):
         assert err is not None and err.code == qe_moe.QE_ERR_STATE and "timed out" in str(err)
         m.check()  # reported once, then cleared
         for _ in range(5):
-            m.forward_normed(0, xd, y, 1)
-            torch.cuda.synchronize()
             try:  # the next forward call reports it, before launching
+                m.forward_stack(0, 2, x8, y8, 8)
+                torch.cuda.synchronize()
                 m.forward_normed(0, xd, y, 1)
             except qe_moe.QeError as ex:
                 assert ex.code == qe_moe.QE_ERR_STATE and "timed out" in str(ex)
