@@ -724,6 +724,14 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
         auto d_prefetch = [&]() {
             if (d_prefetched) return;
             d_prefetched = true;
+            if constexpr (TM == 1) {
+                // wave (item wv / 2, half wv % 2), lane (row lane / 8, block 8 half + lane % 8)
+                const int u = wv >> 1, b = 8 * (wv & 1) + (lane & 7);
+                const uint8_t *drow = arena + (size_t)(s_items[u].x & (QE_N_EXPERT - 1)) * QE_EXPERT_BYTES +
+                                      QE_EXPERT_DOWN_OFF + (size_t)(rb0 + (lane >> 3)) * QE_DN_ROW_BYTES;
+                dpq[0] = *(const uint4 *)(drow + b * 16);
+                dps[0] = ((const uint16_t *)(drow + QE_FF_EXP / 2))[b];
+            } else
 #pragma unroll
             for (int k = 0; k < 2; ++k) {
                 if (half + 8 * k < nitems) {
@@ -895,8 +903,13 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
 #pragma unroll
             for (int i = 0; i < 8; ++i) asm volatile("" : "+v"(wpre.w[i]));
         }
-        if (mode16) { // fp32 h of the 8 pairs -> LDS, then int8 per 32 rows
-            // thread = 4 consecutive h of one pair, 8 lanes per 32-block (quant_x per block)
+        if constexpr (TM == 1) {
+            // Wave (item u = wv / 2, half hw = wv % 2) polls pair u's h words of its
+            // half (elements 256 hw + 4 lane + 0..3), quantises them (8 lanes per
+            // 32-block), and then its lane (row lane / 8, block 8 hw + lane % 8)
+            // forms that block's dot with the item's down row: the routed down of a
+            // wave waits for its own h only, with no workgroup barrier in between.
+            const int u = wv >> 1, hw = wv & 1, b = 8 * hw + (lane & 7);
             static_assert(8 * QE_FF_EXP == 4 * NTH, "h of the 8 pairs: four words per thread");
             uint64_t w[4];
             read_tv<4>(EXr + EX_HF + 4 * tid, 1, tagG, w, true, pc);
@@ -914,6 +927,60 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
             for (int i = 0; i < 4; ++i) q |= (unsigned)(uint8_t)quant_one(h[i], id) << (8 * i);
             *(unsigned *)(s_hq + 4 * tid) = q;
             if ((tid & 7) == 0) s_hs[tid >> 3] = dq;
+            // the other lanes' blocks of this half, written by this wave just above
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            const int8_t *hq = s_hq + u * QE_FF_EXP + b * 32;
+            const uint4 h0 = *(const uint4 *)hq, h1 = *(const uint4 *)(hq + 16);
+            const float hsc = s_hs[u * 16 + b];
+            for (int m = 0; m < d_iters; ++m) {
+                const int rb = (blockIdx.x + m * gridDim.x) * 8;
+                if (rb >= QE_D) break;
+                nl4_blk wq;
+                uint16_t sraw;
+                if (m == 0) { // prefetched during G, decoded before the h wait
+                    wq = wpre;
+                    sraw = (uint16_t)dps[0];
+                } else {
+                    const uint8_t *drow = arena + (size_t)(s_items[u].x & (QE_N_EXPERT - 1)) * QE_EXPERT_BYTES +
+                                          QE_EXPERT_DOWN_OFF + (size_t)(rb + (lane >> 3)) * QE_DN_ROW_BYTES;
+                    wq = nl4_decode_block<true>(*(const uint4 *)(drow + b * 16));
+                    sraw = ((const uint16_t *)(drow + QE_FF_EXP / 2))[b];
+                }
+                const int P = nl4_block_dot(wq, h0, h1);
+                float v = (f16_bits_to_f32(sraw) * hsc) * (float)P;
+                v = v + dpp_f<QE_DPP_XOR1>(v); // the row's 8 blocks of this half
+                v = v + dpp_f<QE_DPP_XOR2>(v);
+                v = v + dpp_f<QE_DPP_HMIRROR>(v);
+                if ((lane & 7) == 0) s_y[(u * 2 + hw) * 8 + (lane >> 3)] = v;
+                __syncthreads();
+                if (tid < 8) { // thread (row k): combine, items in k order
+                    const int k = tid, ro = rb + k;
+                    float yt = 0.f;
+#pragma unroll
+                    for (int it = 0; it < QE_K_USED; ++it) yt += s_wts[it] * (s_y[(it * 2) * 8 + k] + s_y[(it * 2 + 1) * 8 + k]);
+                    const float sd = s_sd[(m * 8 + k) * DEC_T];
+                    const float res = a.residual ? s_res[m * 8 + k] : 0.f;
+                    const float out = (res + s_shg[0] * sd) + yt;
+                    if (last) {
+                        a.x_out[ro] = out;
+                        if (a.sd_out) a.sd_out[ro] = sd;
+                    }
+                    if (!last || EXN) { // the exit norm reads the last x like a next layer would
+#pragma unroll
+                        for (int r = 0; r < REP; ++r) ST_A(dst_x + r * EX_TOTAL + ro, pack_tv(out, tagD));
+                        float *s_gx = (float *)(lds + L_GX);
+                        s_gx[k] = out;
+                        if (k == 0) {
+                            const float g = sumsq_group8(s_gx);
+#pragma unroll
+                            for (int r = 0; r < REP; ++r) ST_A(dst_xs + r * EX_TOTAL + rb / 8, pack_tv(g, tagD));
+                        }
+                    }
+                }
+                __syncthreads(); // s_y is rewritten by the next row group
+            }
         } else {
             for (int task = tid; task < np * 16; task += NTH) { // (pair, 32-block): 8 code words + 1 scale
                 const int p = task >> 4, b = task & 15;
@@ -924,26 +991,21 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
                 dq[1] = make_uint4((unsigned)w[4], (unsigned)w[5], (unsigned)w[6], (unsigned)w[7]);
                 s_hs[task] = tv_val(w[8]);
             }
-        }
-        __syncthreads();
-        for (int m = 0; m < d_iters; ++m) {
-            const int rb = (blockIdx.x + m * gridDim.x) * 8;
-            if (rb >= QE_D) break;
-            const int r = rb + rr;
-            float y[TM];
+            __syncthreads();
+            for (int m = 0; m < d_iters; ++m) {
+                const int rb = (blockIdx.x + m * gridDim.x) * 8;
+                if (rb >= QE_D) break;
+                const int r = rb + rr;
+                float y[TM];
 #pragma unroll
-            for (int t = 0; t < TM; ++t) y[t] = 0.f;
-            for (int k = 0; half + 8 * k < nitems; ++k) {
-                const int s = 4 * k + isub, u = half + 2 * s;
-                const bool act = u < nitems;
-                const int4 it = s_items[act ? u : half];
-                uint4 q;
-                uint16_t sraw;
-                nl4_blk w;
-                if (TM == 1 && m == 0 && k == 0) { // prefetched during G, decoded before the h wait
-                    w = wpre;
-                    sraw = (uint16_t)dps[0];
-                } else {
+                for (int t = 0; t < TM; ++t) y[t] = 0.f;
+                for (int k = 0; half + 8 * k < nitems; ++k) {
+                    const int s = 4 * k + isub, u = half + 2 * s;
+                    const bool act = u < nitems;
+                    const int4 it = s_items[act ? u : half];
+                    uint4 q;
+                    uint16_t sraw;
+                    nl4_blk w;
                     if (m == 0 && k < 2) { // prefetched during G
                         q = k == 0 ? dpq[0] : dpq[1];
                         sraw = (uint16_t)(k == 0 ? dps[0] : dps[1]);
@@ -952,60 +1014,60 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
                         q = *(const uint4 *)(drow + l16 * 16);
                         sraw = ((const uint16_t *)(drow + QE_FF_EXP / 2))[l16];
                     }
-                    w = nl4_decode_block<TM == 1>(q); // T > 1: at the register limit
-                }
-                const float sc = f16_bits_to_f32(sraw);
-                const int npair = act ? it.z : 0;
-                // pairs of the item (<= T), as many rounds as the wave's largest item
-                // needs (wave-uniform: the sums below are cross-lane)
-                for (int j = 0; j < T && __any(j < npair); ++j) {
-                    const bool pj = j < npair;
-                    const int p = pj ? s_pairs[it.y + j] : 0, tp = p / QE_K_USED;
-                    const int8_t *hq = s_hq + p * QE_FF_EXP + l16 * 32;
-                    const int P = nl4_block_dot(w, *(const uint4 *)hq, *(const uint4 *)(hq + 16));
-                    const float v = sum16((sc * s_hs[p * 16 + l16]) * (float)P);
-                    const float vw = pj ? v * s_wts[p] : 0.f;
+                    w = nl4_decode_block<false>(q); // at the register limit
+                    const float sc = f16_bits_to_f32(sraw);
+                    const int npair = act ? it.z : 0;
+                    // pairs of the item (<= T), as many rounds as the wave's largest item
+                    // needs (wave-uniform: the sums below are cross-lane)
+                    for (int j = 0; j < T && __any(j < npair); ++j) {
+                        const bool pj = j < npair;
+                        const int p = pj ? s_pairs[it.y + j] : 0, tp = p / QE_K_USED;
+                        const int8_t *hq = s_hq + p * QE_FF_EXP + l16 * 32;
+                        const int P = nl4_block_dot(w, *(const uint4 *)hq, *(const uint4 *)(hq + 16));
+                        const float v = sum16((sc * s_hs[p * 16 + l16]) * (float)P);
+                        const float vw = pj ? v * s_wts[p] : 0.f;
 #pragma unroll
-                    for (int t = 0; t < TM; ++t) y[t] += t == tp ? vw : 0.f;
-                }
-            }
-#pragma unroll
-            for (int t = 0; t < TM; ++t) {
-                y[t] = add_rows32(add_rows16(y[t]));
-            }
-            if (lane == 0) {
-#pragma unroll
-                for (int t = 0; t < TM; ++t)
-                    if (t < T) s_y[(rr * 2 + half) * DEC_T + t] = y[t];
-            }
-            __syncthreads();
-            if (tid < 8 * T) { // thread (row, token): combine
-                const int k = tid / T, t = tid % T, ro = rb + k;
-                const float sd = s_sd[(m * 8 + k) * DEC_T + t];
-                const float yt = s_y[(k * 2) * DEC_T + t] + s_y[(k * 2 + 1) * DEC_T + t];
-                const float res = a.residual ? s_res[t * 32 + m * 8 + k] : 0.f;
-                const float out = (res + s_shg[t] * sd) + yt;
-                const size_t o = (size_t)t * QE_D + ro;
-                if (last) {
-                    a.x_out[o] = out;
-                    if (a.sd_out) a.sd_out[o] = sd;
-                }
-                if (!last || EXN) { // the exit norm reads the last x like a next layer would
-#pragma unroll
-                    for (int r = 0; r < REP; ++r) ST_A(dst_x + r * EX_TOTAL + o, pack_tv(out, tagD));
-                    // the group's partial of the next norm's sum of squares (an fma
-                    // chain over its 8 rows), gathered in LDS by the thread of row 0;
-                    // these threads are all in wave 0, whose LDS accesses are ordered
-                    float *s_gx = (float *)(lds + L_GX);
-                    s_gx[t * 8 + k] = out;
-                    if (k == 0) {
-                        const float g = sumsq_group8(s_gx + t * 8);
-#pragma unroll
-                        for (int r = 0; r < REP; ++r) ST_A(dst_xs + r * EX_TOTAL + t * 256 + rb / 8, pack_tv(g, tagD));
+                        for (int t = 0; t < TM; ++t) y[t] += t == tp ? vw : 0.f;
                     }
                 }
+#pragma unroll
+                for (int t = 0; t < TM; ++t) {
+                    y[t] = add_rows32(add_rows16(y[t]));
+                }
+                if (lane == 0) {
+#pragma unroll
+                    for (int t = 0; t < TM; ++t)
+                        if (t < T) s_y[(rr * 2 + half) * DEC_T + t] = y[t];
+                }
+                __syncthreads();
+                if (tid < 8 * T) { // thread (row, token): combine
+                    const int k = tid / T, t = tid % T, ro = rb + k;
+                    const float sd = s_sd[(m * 8 + k) * DEC_T + t];
+                    const float yt = s_y[(k * 2) * DEC_T + t] + s_y[(k * 2 + 1) * DEC_T + t];
+                    const float res = a.residual ? s_res[t * 32 + m * 8 + k] : 0.f;
+                    const float out = (res + s_shg[t] * sd) + yt;
+                    const size_t o = (size_t)t * QE_D + ro;
+                    if (last) {
+                        a.x_out[o] = out;
+                        if (a.sd_out) a.sd_out[o] = sd;
+                    }
+                    if (!last || EXN) { // the exit norm reads the last x like a next layer would
+#pragma unroll
+                        for (int r = 0; r < REP; ++r) ST_A(dst_x + r * EX_TOTAL + o, pack_tv(out, tagD));
+                        // the group's partial of the next norm's sum of squares (an fma
+                        // chain over its 8 rows), gathered in LDS by the thread of row 0;
+                        // these threads are all in wave 0, whose LDS accesses are ordered
+                        float *s_gx = (float *)(lds + L_GX);
+                        s_gx[t * 8 + k] = out;
+                        if (k == 0) {
+                            const float g = sumsq_group8(s_gx + t * 8);
+#pragma unroll
+                            for (int r = 0; r < REP; ++r) ST_A(dst_xs + r * EX_TOTAL + t * 256 + rb / 8, pack_tv(g, tagD));
+                        }
+                    }
+                }
+                __syncthreads(); // s_y is rewritten by the next row group
             }
-            __syncthreads(); // s_y is rewritten by the next row group
         }
         __syncthreads(); // the LDS union is rewritten by the next layer's R stage
     }
