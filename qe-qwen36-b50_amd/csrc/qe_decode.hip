@@ -234,7 +234,10 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
 
     const int T = TM == 1 ? 1 : a.T, np = T * QE_K_USED;
     const int d_iters = (QE_D / 8 + gridDim.x - 1) / gridDim.x; // D row groups of 8 per workgroup
-    if (threadIdx.x == 0) s_misc[1] = (int)LD_A(a.sync + SYNC_EPOCH);
+    if (threadIdx.x == 0) {
+        s_misc[1] = (int)LD_A(a.sync + SYNC_EPOCH);
+        s_misc[3] = 0; // T = 1: tag of the layer whose 1/rms is in s_inv (tags are never 0)
+    }
     __syncthreads();
     const unsigned epoch = (unsigned)s_misc[1];
     const PollCtl pc{a.err, a.spin_cap, 1u + (epoch & 0x7fffffffu)};
@@ -305,7 +308,10 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
                                                  (__attribute__((address_space(3))) void *)(rw_lds + 4096 + 256), 2, 0, 0);
             }
         }
-        if (pnorm && wv == 4) { // post_norm -> LDS, 64-element rows padded to 65 words (one dword per lane)
+        // post_norm -> LDS, 64-element rows padded to 65 words (one dword per lane);
+        // T = 1 after the first layer: by wave 0, whose partials poll waits for it
+        // before it signals 1/rms to the threads that scale x as it arrives
+        if (pnorm && wv == (TM == 1 && li > 0 ? 0 : 4)) {
 #pragma unroll
             for (int i = 0; i < 32; ++i)
                 __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)(pnorm + i * 64 + lane),
@@ -314,13 +320,16 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
         // x of a layer li > 0: wave t first polls token t's 256 group partials of
         // the sum of squares (published with x, one word per 8-row group), which
         // give 1/rms at once (canonical order: lane l holds groups 4l..4l+3); then
-        // the whole workgroup reads x, each thread polling its own words.
+        // the whole workgroup reads x, each thread polling its own words (at T = 1
+        // and scaling them: no pass of its own, one barrier fewer).
         if (li > 0 && wv < T) {
             const int t = wv;
             uint64_t w[4];
             read_tv<4>(src_xs + t * 256 + 4 * lane, 1, tagIn, w, true, pc);
             const float ss = wave_sum_canon((tv_val(w[0]) + tv_val(w[1])) + (tv_val(w[2]) + tv_val(w[3])));
             if (lane == 0) s_inv[t] = 1.0f / sqrtf(ss / (float)QE_D + QE_RMS_EPS);
+            if (TM == 1 && lane == 0) // 1/rms, and post_norm (this wave's loads into LDS, waited for by the poll), are in place
+                __hip_atomic_store(&s_misc[3], (int)tagIn, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
         // raw x of all tokens -> LDS (natural layout, token stride 2048; T*2048 = 2 T NTH)
         if (li == 0) {
@@ -346,8 +355,16 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
                 uint64_t w[2];
                 read_tv<2>(src_x + i0 + tid, NTH, tagIn, w, true, pc);
                 const int e0 = i0 + tid, e1 = e0 + NTH;
-                s_xn[(e0 >> 11) * DEC_XSTR + xpos(e0 & 2047)] = tv_val(w[0]);
-                s_xn[(e1 >> 11) * DEC_XSTR + xpos(e1 & 2047)] = tv_val(w[1]);
+                float x0 = tv_val(w[0]), x1 = tv_val(w[1]);
+                if (TM == 1 && pnorm) { // scaled as it arrives, once wave 0 has 1/rms
+                    while (__hip_atomic_load(&s_misc[3], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) != (int)tagIn) {
+                    }
+                    const float inv = s_inv[0];
+                    x0 = (x0 * inv) * s_pn[(e0 >> 6) * 65 + (e0 & 63)];
+                    x1 = (x1 * inv) * s_pn[(e1 >> 6) * 65 + (e1 & 63)];
+                }
+                s_xn[(e0 >> 11) * DEC_XSTR + xpos(e0 & 2047)] = x0;
+                s_xn[(e1 >> 11) * DEC_XSTR + xpos(e1 & 2047)] = x1;
             }
         } else {
             // up to 16 words per thread: 8 polled together per round trip (T = 8: two)
@@ -386,23 +403,31 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
         // RMSNorm in place.  A thread that scales elements of this workgroup's D
         // rows keeps their raw values first (the residual): no other thread
         // writes them.
-        //   T = 1: one element per thread and step; the row tasks below need only
+        //   T = 1: the first layer of a launch, one element per thread and step;
+        //          later layers scaled x as it arrived and carry the residual from
+        //          the previous layer's combine.  The row tasks below need only
         //          this fp32 xn, and its int8 quantisation for the routed units
         //          is done after the barrier by wave 0, which has no row task.
         //   T > 1: 8 elements per thread, scaled and quantised (4 lanes per
         //          32-block) in one pass.
         if constexpr (TM == 1) {
-            for (int e = tid; e < QE_D; e += NTH) {
-                float *px = s_xn + xpos(e);
-                float v = *px;
-                if (a.residual)
-                    for (int m = 0; m < d_iters; ++m)
-                        if ((e >> 3) == (int)blockIdx.x + m * (int)gridDim.x) s_res[m * 8 + (e & 7)] = v;
-                if (pnorm) {
-                    v = (v * s_inv[0]) * s_pn[(e >> 6) * 65 + (e & 63)];
-                    *px = v;
+            if (li == 0) {
+                for (int e = tid; e < QE_D; e += NTH) {
+                    float *px = s_xn + xpos(e);
+                    float v = *px;
+                    if (a.residual)
+                        for (int m = 0; m < d_iters; ++m)
+                            if ((e >> 3) == (int)blockIdx.x + m * (int)gridDim.x) s_res[m * 8 + (e & 7)] = v;
+                    if (pnorm) {
+                        v = (v * s_inv[0]) * s_pn[(e >> 6) * 65 + (e & 63)];
+                        *px = v;
+                    }
+                    if (last && blockIdx.x == 0 && a.xn_out) a.xn_out[e] = v;
                 }
-                if (last && blockIdx.x == 0 && a.xn_out) a.xn_out[e] = v;
+                __syncthreads();
+            } else if (last && blockIdx.x == 0 && a.xn_out && wv == NWV - 1) {
+                // (a wave without a row task: a store of wave 0's own would hold up its logits poll)
+                for (int e = lane; e < QE_D; e += 64) a.xn_out[e] = s_xn[xpos(e)];
             }
         } else {
             for (int w = tid; w < T * 256; w += NTH) {
@@ -431,8 +456,8 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
                     o[1] = make_float4(v[4], v[5], v[6], v[7]);
                 }
             }
+            __syncthreads();
         }
-        __syncthreads();
         for (int task = task0; task < N_RTASK; task += (int)gridDim.x * (NWV - TW0)) {
             const bool in_lds = rw_pref && task == task0;
             if (task < QE_ROUTER_ROWS) {
@@ -963,6 +988,7 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
                     const float sd = s_sd[(m * 8 + k) * DEC_T];
                     const float res = a.residual ? s_res[m * 8 + k] : 0.f;
                     const float out = (res + s_shg[0] * sd) + yt;
+                    if (a.residual) s_res[m * 8 + k] = out; // the next layer's residual (its x)
                     if (last) {
                         a.x_out[ro] = out;
                         if (a.sd_out) a.sd_out[ro] = sd;
