@@ -547,8 +547,9 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
             // workgroup barrier that follows the top-8), by wave 0 before it polls
             // the logits: 8 elements per lane and step, 4 lanes per 32-block
             if (wv == 0) {
-                for (int w = lane; w < 256; w += 64) {
-                    const int e = 8 * w;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) { // unrolled: the four blocks' chains overlap
+                    const int w = lane + 64 * j, e = 8 * w;
                     float v[8];
 #pragma unroll
                     for (int i = 0; i < 8; ++i) v[i] = s_xn[xpos(e + i)];
