@@ -1026,21 +1026,34 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
                 float y[TM];
 #pragma unroll
                 for (int t = 0; t < TM; ++t) y[t] = 0.f;
+                // round k's down row block, loaded a round ahead (unconditionally: a
+                // round past the items re-reads a valid row, never used, so the
+                // compiler's waits stay per load)
+                // (round 1 was prefetched during G too; read again here it comes from the
+                // cache, and the load stays unconditional)
+                auto d_row = [&](int k, uint4 &q, unsigned &sr) {
+                    const int u = half + 2 * (4 * k + isub);
+                    const int4 it = s_items[u < nitems ? u : half];
+                    const uint8_t *drow = arena + (size_t)it.x * QE_EXPERT_BYTES + QE_EXPERT_DOWN_OFF + (size_t)r * QE_DN_ROW_BYTES;
+                    q = *(const uint4 *)(drow + l16 * 16);
+                    sr = ((const uint16_t *)(drow + QE_FF_EXP / 2))[l16];
+                };
+                uint4 qn;
+                unsigned sn;
+                if (m == 0) { // prefetched during G
+                    qn = dpq[0];
+                    sn = dps[0];
+                } else {
+                    d_row(0, qn, sn);
+                }
                 for (int k = 0; half + 8 * k < nitems; ++k) {
                     const int s = 4 * k + isub, u = half + 2 * s;
                     const bool act = u < nitems;
                     const int4 it = s_items[act ? u : half];
-                    uint4 q;
-                    uint16_t sraw;
+                    const uint4 q = qn;
+                    const uint16_t sraw = (uint16_t)sn;
+                    d_row(k + 1, qn, sn);
                     nl4_blk w;
-                    if (m == 0 && k < 2) { // prefetched during G
-                        q = k == 0 ? dpq[0] : dpq[1];
-                        sraw = (uint16_t)(k == 0 ? dps[0] : dps[1]);
-                    } else {
-                        const uint8_t *drow = arena + (size_t)it.x * QE_EXPERT_BYTES + QE_EXPERT_DOWN_OFF + (size_t)r * QE_DN_ROW_BYTES;
-                        q = *(const uint4 *)(drow + l16 * 16);
-                        sraw = ((const uint16_t *)(drow + QE_FF_EXP / 2))[l16];
-                    }
                     w = nl4_decode_block<false>(q); // at the register limit
                     const float sc = f16_bits_to_f32(sraw);
                     const int npair = act ? it.z : 0;
