@@ -67,6 +67,7 @@ QE_DEV int xpos(int e) { return (e & 31) * 65 + (e >> 5); } // raw x element e o
 #define L_HQ (L_U + 64 * 8 * 4)                     //   D: int8 [T*8][512] quantised h
 #define L_HS (L_HQ + DEC_T * 8 * QE_FF_EXP)         //   D: f32 [T*8][16] its block scales
 #define L_Y (L_HS + DEC_T * 8 * 16 * 4)             //   D: f32 [8 rows][2 halves][T] routed partials
+#define L_YG (L_Y + 8 * 2 * DEC_T * 4)              //   D, T > 1: f32 [16 waves][4 lane groups][T] their running sums
 #define L_U_END (L_U + DEC_T * DEC_XSTR * 4)
 #define L_XQ L_U_END                                // int8 [T][2048]   quantised xn
 #define L_XS (L_XQ + DEC_T * QE_D)                  // f32 [T][64]      its block scales
@@ -89,7 +90,7 @@ QE_DEV int xpos(int e) { return (e & 31) * 65 + (e >> 5); } // raw x element e o
 #define L_LG (L_TK + 256 * 8 + 256 * 4 + 8 * 4 + 16) // f32 [T][257] the last layer's logits (routing sink)
 #define L_IORD (L_LG + DEC_T * QE_ROUTER_ROWS * 4)   // int [64] T > 1: items in unit deal order
 #define L_TOTAL (L_IORD + 64 * 4)
-static_assert(L_Y + 8 * 2 * DEC_T * 4 <= L_U_END, "D-stage LDS must fit in the union");
+static_assert(L_YG + NWV * 4 * DEC_T * 4 <= L_U_END, "D-stage LDS must fit in the union");
 static_assert(64 * 8 * 4 <= L_HQ - L_U, "G-stage LDS must fit in front of the D buffers");
 static_assert(L_TOTAL <= 160 * 1024, "LDS budget of one workgroup per CU");
 
@@ -1023,9 +1024,11 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
                 const int rb = (blockIdx.x + m * gridDim.x) * 8;
                 if (rb >= QE_D) break;
                 const int r = rb + rr;
-                float y[TM];
-#pragma unroll
-                for (int t = 0; t < TM; ++t) y[t] = 0.f;
+                // this lane group's per-token sums, in LDS: one add per pair (from the
+                // group's first lane, in program order) instead of a select and an add
+                // per token in every lane
+                float *s_yg = (float *)(lds + L_YG) + (wv * 4 + isub) * DEC_T;
+                if (l16 < DEC_T) s_yg[l16] = 0.f;
                 // round k's down row block, loaded a round ahead (unconditionally: a
                 // round past the items re-reads a valid row, never used, so the
                 // compiler's waits stay per load)
@@ -1065,19 +1068,13 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
                         const int8_t *hq = s_hq + p * QE_FF_EXP + l16 * 32;
                         const int P = nl4_block_dot(w, *(const uint4 *)hq, *(const uint4 *)(hq + 16));
                         const float v = sum16((sc * s_hs[p * 16 + l16]) * (float)P);
-                        const float vw = pj ? v * s_wts[p] : 0.f;
-#pragma unroll
-                        for (int t = 0; t < TM; ++t) y[t] += t == tp ? vw : 0.f;
+                        if (pj && l16 == 0)
+                            __hip_atomic_fetch_add(s_yg + tp, v * s_wts[p], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
                     }
                 }
-#pragma unroll
-                for (int t = 0; t < TM; ++t) {
-                    y[t] = add_rows32(add_rows16(y[t]));
-                }
-                if (lane == 0) {
-#pragma unroll
-                    for (int t = 0; t < TM; ++t)
-                        if (t < T) s_y[(rr * 2 + half) * DEC_T + t] = y[t];
+                if (lane < T) { // the wave's four lane groups, in order
+                    const float *g = (const float *)(lds + L_YG) + wv * 4 * DEC_T + lane;
+                    s_y[(rr * 2 + half) * DEC_T + lane] = ((g[0] + g[DEC_T]) + g[2 * DEC_T]) + g[3 * DEC_T];
                 }
                 __syncthreads();
                 if (tid < 8 * T) { // thread (row, token): combine
