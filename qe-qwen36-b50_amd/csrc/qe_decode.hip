@@ -49,7 +49,6 @@
 #define DEC_T QE_SMALL_T
 #define NWV 16            /* waves per workgroup */
 #define NTH (NWV * 64)
-#define DEC_PFI 16        /* items whose down rows are prefetched into registers during G */
 #define SYNC_EPOCH 0
 #define SYNC_EXIT 32
 #define REP QE_DEC_REP      /* copies of every exchanged buffer and counter */
@@ -253,7 +252,9 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
         int tid = threadIdx.x;
         asm volatile("" : "+v"(tid));
         const int lane = tid & 63, wv = tid >> 6, l16 = lane & 15;
-        // D: wave = (row rr of the group of 8, half); items u = half + 2 s, slot s = 4 k + isub
+        // D (shared down rows, and the T > 1 routed down): wave = (row rr of the group
+        // of 8, half); items u = half + 2 s, slot s = 4 k + isub.  The T = 1 routed
+        // down has its own layout (wave = item wv / 2, half wv % 2).
         const int rr = wv >> 1, half = wv & 1, isub = lane >> 4;
         const int l = a.first_layer + li;
         const bool last = li == a.n_layers - 1;
@@ -739,10 +740,13 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
         if (TM != 1) __syncthreads();
         const int nitems = s_misc[0];
 
-        // Down rows of this workgroup's first D row group for the first DEC_PFI
-        // items and the wave's shared down row, loaded into registers during G
-        // (after the first unit's own loads, so the unit does not wait for them).
-        // Wave (row rr, half), round k: lane (isub, block) takes item half + 2 (4 k + isub).
+        // Down rows of this workgroup's first D row group for the first items and
+        // the wave's shared down row, loaded into registers during G (after the
+        // first unit's own loads, so the unit does not wait for them).
+        //   T = 1: wave (item wv / 2, half wv % 2), lane (row lane / 8, block
+        //          8 half + lane % 8): the block its routed down needs first.
+        //   T > 1: wave (row rr, half), round k < 2: lane (isub, block) takes item
+        //          half + 2 (4 k + isub).
         uint4 dpq[2] = {make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0)};
         unsigned dps[2] = {0u, 0u};
         uint4 dq0 = make_uint4(0, 0, 0, 0), dq1 = dq0;
