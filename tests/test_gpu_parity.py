@@ -399,7 +399,9 @@ def test_short_stack_every_batch(torch_cuda, T):
     between the two the 40-layer test covers: x crosses the exchange 2, 4, 6, 8,
     10, 12 or 14 words per thread (polled in rounds of 8, then 4 and 2), and the
     stack equals the layer-by-layer chain bit for bit, each layer matching the
-    oracle on the GPU's own input."""
+    oracle on the GPU's own input.  A second launch on the same input repeats
+    the first bit for bit (the routed down sums per lane group in LDS, the
+    exchanges: nothing depends on timing)."""
     torch = torch_cuda
     n, seed = 3, SEED + 3300 + T
     m = qe_moe.MoE(n_layers=n, t_max=8)
@@ -414,6 +416,10 @@ def test_short_stack_every_batch(torch_cuda, T):
         torch.cuda.synchronize()
         m.check()
         stack_gpu = x_out.cpu().numpy()
+        m.forward_stack(0, n, x_in, x_out, T)
+        torch.cuda.synchronize()
+        m.check()
+        assert np.array_equal(x_out.cpu().numpy().view(np.uint32), stack_gpu.view(np.uint32)), "repeat launch differs"
         h = x0
         for l in range(n):
             L = O.SynthLayer(seed, l)
