@@ -745,7 +745,7 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
         // first unit's own loads, so the unit does not wait for them).
         //   T = 1: wave (item wv / 2, half wv % 2), lane (row lane / 8, block
         //          8 half + lane % 8): the block its routed down needs first.
-        //   T > 1: wave (row rr, half), round 0: lane (isub, block) takes item
+        //   T > 1: wave (row rr, half), item round k = 0: lane (isub, block) takes item
         //          half + 2 isub.
         uint4 dpq[1] = {make_uint4(0, 0, 0, 0)};
         unsigned dps[1] = {0u};
@@ -762,7 +762,7 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
                                       QE_EXPERT_DOWN_OFF + (size_t)(rb0 + (lane >> 3)) * QE_DN_ROW_BYTES;
                 dpq[0] = *(const uint4 *)(drow + b * 16);
                 dps[0] = ((const uint16_t *)(drow + QE_FF_EXP / 2))[b];
-            } else if (half < nitems) { // round 0 (the routed down loads each next round itself)
+            } else if (half < nitems) { // item round k = 0 (the routed down loads each later one itself)
                 int u = half + 2 * isub;
                 if (u >= nitems) u = half; // a valid item; the slot is never used
                 const uint8_t *drow = arena + (size_t)s_items[u].x * QE_EXPERT_BYTES + QE_EXPERT_DOWN_OFF +
@@ -1031,7 +1031,7 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
                 if (l16 < DEC_T) s_yg[l16] = 0.f;
                 // round k's down row block, loaded a round ahead (unconditionally: a
                 // round past the items re-reads a valid row, never used, so the
-                // compiler's waits stay per load); round 0 came during G
+                // compiler's waits stay per load); item round k = 0 came during G
                 auto d_row = [&](int k, uint4 &q, unsigned &sr) {
                     const int u = half + 2 * (4 * k + isub);
                     const int4 it = s_items[u < nitems ? u : half];
