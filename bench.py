@@ -184,6 +184,29 @@ def convert_bench(torch, qe_moe, steps, cpu_experts, threads):
     return res
 
 
+def cpu_host(threads):
+    """The host CPU the baseline ran on, from lscpu: model, sockets, cores per
+    socket, threads per core, logical CPUs, and how many of them this process
+    may use (its affinity: the box's CPU share) and used (threads)."""
+    info = {}
+    try:
+        import subprocess
+
+        txt = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=20).stdout
+        kv = {l.split(":", 1)[0].strip(): l.split(":", 1)[1].strip() for l in txt.splitlines() if ":" in l}
+        info = {"model": kv.get("Model name"), "sockets": kv.get("Socket(s)"), "cores_per_socket": kv.get("Core(s) per socket"),
+                "threads_per_core": kv.get("Thread(s) per core"), "logical_cpus": kv.get("CPU(s)"),
+                "hypervisor": kv.get("Hypervisor vendor")}
+    except (OSError, ValueError):
+        pass
+    try:
+        info["affinity_cpus"] = len(os.sched_getaffinity(0))
+    except OSError:
+        pass
+    info["threads_used"] = threads
+    return info
+
+
 def pmc_traffic(path):
     """HBM bytes per k_decode dispatch from the committed rocprofv3 --pmc summary
     (FETCH_SIZE and WRITE_SIZE in KiB per dispatch, each divided by the factor
@@ -255,7 +278,7 @@ def main():
     if not args.no_decode:
         # ---------------- config 2: 40-layer decode, B=1 ----------------
         log("building 40-layer arena (18.12 GB) from the seeded generator")
-        m = qe_moe.MoE(n_layers=N_LAYERS, t_max=8)
+        m = qe_moe.MoE(n_layers=N_LAYERS, t_max=16)
         for l in range(N_LAYERS):
             m.synth_layer(l, SEED, None, stream=stream)
         x = torch.empty(1, 2048, device=dev)
@@ -312,7 +335,10 @@ def main():
         torch.cuda.synchronize()
         prof = m.profile_read()
         m.profile(False)
-        kernels = {k: {"avg_us": round(v[0] / v[1] * 1e3, 3), "launches": v[1]} for k, v in prof.items()}
+        kernels = {"source": "the library's per-launch HIP event pairs (qe_moe_profile) over a separate 20-step pass, "
+                             "not the timed loop: each bracketed launch pays the events' own cost; roofline.avg_us "
+                             "and profiles/k_decode_cfg2_kernel_stats.txt (rocprofv3) are the kernel's duration",
+                   **{k: {"avg_us": round(v[0] / v[1] * 1e3, 3), "launches": v[1]} for k, v in prof.items()}}
 
         # config 0: one layer, B=1, rotated over the 40 resident layers
         x1 = torch.empty(1, 2048, device=dev)
@@ -336,6 +362,24 @@ def main():
         stack40_b8 = {"tokens_per_s": round(8000.0 / ms8, 1), "ms_per_step": round(ms8, 4),
                       "note": "8 tokens per step through the 40-layer stack, no router bias (not BASELINE config 1)"}
 
+        # one layer per call at T = 8 (the persistent decode kernel), 9, 12 and 16
+        # (the prefill launches), no bias, rotated over the 40 layers: where the
+        # two plans cross (the reference switches to its GEMV rounds below 16
+        # tokens, engine/qe.cpp:2008-2027)
+        small_t = {}
+        for T_ in (8, 9, 12, 16):
+            xs_ = torch.empty(T_, 2048, device=dev)
+            qe_moe.synth_x(SEED, 20 + T_, xs_, xs_.numel(), stream=stream)
+            ys_ = torch.empty_like(xs_)
+            u_ = []
+            for l in range(N_LAYERS):
+                m.forward_normed(l, xs_, ys_, T_, stream=stream)
+                u_.append(int(np.count_nonzero(np.diff(m.routing(T_, stream=stream)["off"]))))
+            ms_ = layer_rotation(torch, m, xs_, ys_, T_, N_LAYERS, max(100, args.steps // 2))
+            small_t[str(T_)] = {"us_per_call": round(ms_ * 1e3, 3), "tokens_per_s": round(T_ * 1000.0 / ms_, 1),
+                                "distinct_experts_mean": round(float(np.mean(u_)), 2),
+                                "plan": "k_decode (persistent)" if T_ <= 8 else "prefill launches"}
+
         # config 1: one layer, B=8, Zipf s=1 router bias, rotated over the 40 layers
         for l in range(N_LAYERS):
             m.set_dense(l, bias=qe_moe.synth_zipf_bias(SEED, l, 1.0), stream=stream)
@@ -356,7 +400,7 @@ def main():
         del m
         torch.cuda.empty_cache()
         dec = dict(tok_s=tok_s, ms=ms, graph_used=graph_used, dec_avg_s=dec_avg_s, dec_bytes=dec_bytes,
-                   achieved=achieved, kernels=kernels, cfg0=cfg0, cfg1=cfg1, stack40_b8=stack40_b8)
+                   achieved=achieved, kernels=kernels, cfg0=cfg0, cfg1=cfg1, stack40_b8=stack40_b8, small_t=small_t)
 
     # ---------------- config 3: prefill 512, one layer ----------------
     pre = {}
@@ -397,11 +441,14 @@ def main():
                                           "tops": round(routed_flop / g_s / 1e12, 2), "mfma": "i32_16x16x32_i8",
                                           "frac_int8_peak": round(routed_flop / g_s / INT8_PEAK, 4),
                                           "frac_fp16_peak": round(routed_flop / g_s / FP16_PEAK, 4),
-                                          "note": "time includes the shared-expert down tiles (1.07 GFLOP) of the same launch"},
+                                          "note": "time includes the shared-expert down tiles (1.07 GFLOP) of the same launch",
+                                          "source": "per-launch HIP event pairs of the library profiler over 5 calls after "
+                                                    "the timed loop (rocprofv3 durations: profiles/prefill512_zipf1_kernel_stats.txt)"},
                "prefill512_routing": {"distinct_experts": int(np.count_nonzero(cnt)), "max_tokens_per_expert": int(cnt.max()),
                                       "top8_share": round(float(np.sort(cnt)[-8:].sum() / cnt.sum()), 4),
                                       "experts_lt4_tokens": int(((cnt > 0) & (cnt < 4)).sum())},
-               "prefill512_kernels_us": {k: round(v[0] / v[1] * 1e3, 2) for k, v in pk.items()}}
+               "prefill512_kernels_us": {"source": "per-launch HIP event pairs of the library profiler, 5 calls",
+                                         **{k: round(v[0] / v[1] * 1e3, 2) for k, v in pk.items()}}}
         del mp, xp, yp
         torch.cuda.empty_cache()
 
@@ -435,7 +482,8 @@ def main():
             gf, cms, ncall = cpu_prefill(T_, inst, s_, threads, args.cpu_seconds / 2)
             entry = {"value": round(gf, 2), "unit": "GFLOP/s", "ms_per_call": round(cms, 1), "cores": threads,
                      "kind": "port", "sample": f"{ncall} call(s) of the same {T_}-token layer (all 256 experts), "
-                                               "the reference's batched CPU expert path"}
+                                               "the reference's batched CPU expert path (weights decoded once per "
+                                               "group of 4 pairs, cpu_dot_nl4_x4)", "host": cpu_host(threads)}
             if key == "prefill512":
                 pre["prefill512_cpu_baseline"] = entry
             else:
@@ -445,6 +493,8 @@ def main():
     if not args.no_convert:
         log("converter: one layer of Q8_0 experts")
         conv = convert_bench(torch, qe_moe, 5, 0 if args.no_cpu_baseline else 4, threads)
+        if conv.get("cpu_baseline"):
+            conv["cpu_baseline"]["host"] = cpu_host(threads)
         torch.cuda.empty_cache()
 
     # ---------------- CPU baseline ----------------
@@ -459,10 +509,7 @@ def main():
         if threads != 12:  # the reference's default pool size (engine/qe.cpp:1201)
             t12, s12, n12 = cpu_baseline(args.cpu_layers, args.cpu_seconds / 2, 100000, 12)
             cpu["threads_12"] = {"value": round(t12, 3), "tokens": n12, "seconds": round(s12, 2)}
-        try:
-            cpu["cpu_model"] = [l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo") if l.startswith("model name")][0]
-        except (OSError, IndexError):
-            pass
+        cpu["host"] = cpu_host(threads)
 
     traffic = pmc_traffic(os.path.join(REPO, TRAFFIC_FILE))
     if dec is None:  # prefill-only run (profiling): no headline line
@@ -485,10 +532,11 @@ def main():
                      "bytes_per_launch": dec_bytes,
                      "avg_us": round(dec_avg_s * 1e6, 3),
                      "avg_us_source": "timed region / steps (one k_decode launch per step, HIP events on its stream)"},
-        "kernels": dec["kernels"],
+        "event_profiler_pass": dec["kernels"],
         "cfg0_decode_b1_layer": dec["cfg0"],
         "cfg1_decode_b8_zipf_layer": dec["cfg1"],
         "stack40_b8": dec["stack40_b8"],
+        "layer_small_batch": {"note": "one layer per call, T tokens, no bias, calls rotated over 40 layers", **dec["small_t"]},
         "convert_layer_q8_0": conv,
         "cpu_baseline": cpu,
     }

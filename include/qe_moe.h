@@ -127,7 +127,11 @@ int qe_moe_dispatch(qe_moe_ctx *ctx, const int32_t *ids, int T, void *stream);
  * library holds on every device it runs on until the process ends, sized for
  * T <= QE_MOE_DISPATCH_NOALLOC_T_MAX; larger T returns QE_ERR_ARG.  Every call
  * on one device shares that array: calls that overlap on one device (other
- * streams, other threads) race. */
+ * streams, other threads) race.  Under HIP graph capture: the array's address
+ * on a device is looked up once, by qe_moe_create for its device or else by
+ * the first call on that device, and the lookup must not run while a stream
+ * is capturing: create a context on the device, or make one call, before
+ * capturing the first one. */
 #define QE_MOE_DISPATCH_NOALLOC_T_MAX 16384
 int qe_moe_dispatch_noalloc(const int32_t *ids, int T, int32_t *off, int32_t *pairs, void *stream);
 

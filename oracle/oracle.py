@@ -55,6 +55,7 @@ def load():
         "orc_quant_x_avx2": (None, [vp, i32, vp, vp]),
         "orc_dot_nl4": (f32, [vp, i32, vp, vp]),
         "orc_dot_nl4_avx2": (f32, [vp, i32, vp, vp]),
+        "orc_dot_nl4_x4_avx2": (None, [vp, i32, vp, vp, i32, vp]),
         "orc_canon_dot": (f32, [vp, vp]),
         "orc_canon_sumsq": (f32, [vp]),
         "orc_rmsnorm": (None, [vp, vp, i32, vp]),
@@ -134,6 +135,19 @@ def quant_x(x, avx2=False):
 def dot_nl4(row, cols, xq, xs, avx2=False):
     f = load().orc_dot_nl4_avx2 if avx2 else load().orc_dot_nl4
     return f(_p(np.ascontiguousarray(row)), cols, _p(np.ascontiguousarray(xq)), _p(np.ascontiguousarray(xs)))
+
+
+def dot_nl4_x4(row, cols, xqs, xss):
+    """row . x_t for up to four quantised activation rows, weights decoded once per block."""
+    n = len(xqs)
+    xqs = [np.ascontiguousarray(q) for q in xqs]
+    xss = [np.ascontiguousarray(s) for s in xss]
+    qp = (ctypes.c_void_p * 4)(*[q.ctypes.data for q in xqs], *([None] * (4 - n)))
+    sp = (ctypes.c_void_p * 4)(*[s.ctypes.data for s in xss], *([None] * (4 - n)))
+    out = np.zeros(4, np.float32)
+    load().orc_dot_nl4_x4_avx2(_p(np.ascontiguousarray(row)), cols, ctypes.cast(qp, ctypes.c_void_p),
+                               ctypes.cast(sp, ctypes.c_void_p), n, _p(out))
+    return out[:n]
 
 
 def canon_dot(a, b):

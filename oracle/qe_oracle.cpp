@@ -176,6 +176,39 @@ ORC_API float orc_dot_nl4_avx2(const uint8_t *row, int cols, const int8_t *xq, c
     return hsum8(a);
 }
 
+// The same dot for n <= 4 activation rows at once, each weight block decoded
+// once for all of them (the reference's cpu_dot_nl4_x4, engine/qe.cpp:722-741,
+// which its batched cold-expert path calls per group of four pairs,
+// :2064-2072 and :2090-2097).  Every token keeps its own eight-lane
+// accumulator and its own dw * xs[b] product, so out[t] equals
+// orc_dot_nl4_avx2(row, cols, xq[t], xs[t]) bit for bit.
+ORC_API void orc_dot_nl4_x4_avx2(const uint8_t *row, int cols, const int8_t *const *xq, const float *const *xs, int n,
+                                 float *out) {
+    const uint16_t *sc = (const uint16_t *)(row + cols / 2);
+    const __m128i tbl = _mm_loadu_si128((const __m128i *)QE_KVALUES_NL4);
+    const __m128i m4 = _mm_set1_epi8(0x0f);
+    const __m256i ones = _mm256_set1_epi16(1);
+    __m256 acc[4];
+    for (int t = 0; t < 4; ++t) acc[t] = _mm256_setzero_ps();
+    for (int b = 0; b < cols / 32; ++b) {
+        const __m128i raw = _mm_loadu_si128((const __m128i *)(row + b * 16));
+        const __m256i w = _mm256_set_m128i(_mm_shuffle_epi8(tbl, _mm_and_si128(_mm_srli_epi16(raw, 4), m4)),
+                                           _mm_shuffle_epi8(tbl, _mm_and_si128(raw, m4)));
+        const __m256i wabs = _mm256_sign_epi8(w, w);
+        const float dw = _cvtsh_ss(sc[b]);
+        for (int t = 0; t < n; ++t) {
+            const __m256i xv = _mm256_loadu_si256((const __m256i *)(xq[t] + b * 32));
+            const __m256i p = _mm256_madd_epi16(_mm256_maddubs_epi16(wabs, _mm256_sign_epi8(xv, w)), ones);
+            acc[t] = _mm256_fmadd_ps(_mm256_set1_ps(dw * xs[t][b]), _mm256_cvtepi32_ps(p), acc[t]);
+        }
+    }
+    for (int t = 0; t < n; ++t) {
+        float a[8];
+        _mm256_storeu_ps(a, acc[t]);
+        out[t] = hsum8(a);
+    }
+}
+
 // ---------------------------------------------------------------------------
 // canonical fp32 dot of length 2048 (router rows):
 //   64 chunks of 32 contiguous elements, each an fma chain from 0 in index
@@ -367,9 +400,11 @@ ORC_API void orc_combine(const float *x2, const float *shg, const float *sd, con
 // ---------------------------------------------------------------------------
 // CPU baseline: one full layer with a thread pool, the reference's batched
 // cold-expert structure (qe.cpp:2050-2101): per routed expert, 32-row gate/up
-// tasks and 128-row down tasks from an atomic queue; each weight row is
-// decoded once per group of its tokens.  Router, top-8, dispatch, shared
-// expert and combine run on the same threads.
+// tasks and 128-row down tasks from a dynamic queue; within a row the expert's
+// pairs go in groups of up to four (dispatch order), and each weight block is
+// decoded once per group (orc_dot_nl4_x4_avx2, the reference's
+// cpu_dot_nl4_x4).  Router, top-8, dispatch, shared expert and combine run on
+// the same threads.
 // ---------------------------------------------------------------------------
 struct BaselineLayer {
     const float *router;    /* 257 x 2048 */
@@ -429,11 +464,19 @@ ORC_API double orc_baseline_layer(const float *x2, const float *post_norm, const
         const int e = act[task / (FF / RB)], r0 = (task % (FF / RB)) * RB;
         const uint8_t *base = experts[e];
         for (int r = r0; r < r0 + RB; ++r)
-            for (int k = off[e]; k < off[e + 1]; ++k) {
-                const int p = pairs[k], t = p / K;
-                const float g = orc_dot_nl4_avx2(base + (size_t)r * QE_GU_ROW_BYTES, D, xq.data() + (size_t)t * D, xs.data() + (size_t)t * (D / 32));
-                const float u = orc_dot_nl4_avx2(base + (size_t)(FF + r) * QE_GU_ROW_BYTES, D, xq.data() + (size_t)t * D, xs.data() + (size_t)t * (D / 32));
-                h[(size_t)p * FF + r] = g / (1.f + expf(-g)) * u;
+            for (int k = off[e]; k < off[e + 1]; k += 4) {
+                const int n = std::min(4, off[e + 1] - k);
+                const int8_t *xqg[4];
+                const float *xsg[4];
+                for (int i = 0; i < n; ++i) {
+                    const int t = pairs[k + i] / K;
+                    xqg[i] = xq.data() + (size_t)t * D;
+                    xsg[i] = xs.data() + (size_t)t * (D / 32);
+                }
+                float g[4], u[4];
+                orc_dot_nl4_x4_avx2(base + (size_t)r * QE_GU_ROW_BYTES, D, xqg, xsg, n, g);
+                orc_dot_nl4_x4_avx2(base + (size_t)(FF + r) * QE_GU_ROW_BYTES, D, xqg, xsg, n, u);
+                for (int i = 0; i < n; ++i) h[(size_t)pairs[k + i] * FF + r] = g[i] / (1.f + expf(-g[i])) * u[i];
             }
     }
 #pragma omp parallel for schedule(static)
@@ -451,9 +494,18 @@ ORC_API double orc_baseline_layer(const float *x2, const float *post_norm, const
         const int e = act[task / (D / RD)], r0 = (task % (D / RD)) * RD;
         const uint8_t *down = experts[e] + QE_EXPERT_DOWN_OFF;
         for (int r = r0; r < r0 + RD; ++r)
-            for (int k = off[e]; k < off[e + 1]; ++k) {
-                const int p = pairs[k];
-                yp[(size_t)p * D + r] = wts[p] * orc_dot_nl4_avx2(down + (size_t)r * QE_DN_ROW_BYTES, FF, hq.data() + (size_t)p * FF, hs.data() + (size_t)p * (FF / 32));
+            for (int k = off[e]; k < off[e + 1]; k += 4) {
+                const int n = std::min(4, off[e + 1] - k);
+                const int8_t *hqg[4];
+                const float *hsg[4];
+                for (int i = 0; i < n; ++i) {
+                    const int p = pairs[k + i];
+                    hqg[i] = hq.data() + (size_t)p * FF;
+                    hsg[i] = hs.data() + (size_t)p * (FF / 32);
+                }
+                float y[4];
+                orc_dot_nl4_x4_avx2(down + (size_t)r * QE_DN_ROW_BYTES, FF, hqg, hsg, n, y);
+                for (int i = 0; i < n; ++i) yp[(size_t)pairs[k + i] * D + r] = wts[pairs[k + i]] * y[i];
             }
     }
     orc_combine(post_norm ? x2 : nullptr, shg.data(), sd.data(), yp.data(), T, out);

@@ -203,6 +203,11 @@ int qe_moe_create(int device, int n_layers, int t_max, qe_moe_ctx **out) {
         delete c;
         return fail(QE_ERR_HIP, "qe_moe_create: initial memset failed");
     }
+    if (qe_noalloc_prepare(nullptr) != hipSuccess) { // the no-allocation dispatch's scratch, looked up before any capture
+        free_all(c);
+        delete c;
+        return fail(QE_ERR_HIP, "qe_moe_create: lookup of the static dispatch scratch failed");
+    }
     *out = c;
     return QE_OK;
 }
@@ -237,10 +242,14 @@ int qe_moe_set_dense(qe_moe_ctx *c, int layer, const float *post_norm, const flo
     const hipMemcpyKind k = on_dev ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice;
     hipStream_t s = (hipStream_t)stream;
     const QeLayerPtrs L = layer_ptrs(c, layer);
+    // a tensor being replaced counts as missing until its copy has gone through:
+    // a failed copy leaves the layer refused (QE_ERR_STATE), not running on
+    // half-written weights
+    const unsigned bits = (post_norm ? HAVE_NORM : 0u) | (router ? HAVE_ROUTER : 0u) | (sh_gu ? HAVE_SH_GU : 0u) |
+                          (sh_down ? HAVE_SH_DN : 0u);
+    c->have[layer] &= ~bits;
     if (post_norm) HIP_TRY(hipMemcpyAsync((void *)L.post_norm, post_norm, QE_D * 4, k, s));
     if (router) HIP_TRY(hipMemcpyAsync((void *)L.router, router, QE_ROUTER_BYTES, k, s));
-    c->have[layer] |= (post_norm ? HAVE_NORM : 0u) | (router ? HAVE_ROUTER : 0u) | (sh_gu ? HAVE_SH_GU : 0u) |
-                      (sh_down ? HAVE_SH_DN : 0u);
     if (bias) {
         HIP_TRY(hipMemcpyAsync(c->bias + (size_t)layer * QE_N_EXPERT, bias, QE_N_EXPERT * 4, k, s));
         c->has_bias[layer] = 1;
@@ -249,6 +258,7 @@ int qe_moe_set_dense(qe_moe_ctx *c, int layer, const float *post_norm, const flo
     if (sh_gu) HIP_TRY(hipMemcpyAsync((void *)L.sh_gu, sh_gu, QE_SH_GU_BYTES, k, s));
     if (sh_down) HIP_TRY(hipMemcpyAsync((void *)L.sh_dn, sh_down, QE_SH_DN_BYTES, k, s));
     if (!on_dev) HIP_TRY(hipStreamSynchronize(s)); /* host sources need not outlive the call */
+    c->have[layer] |= bits;
     return QE_OK;
 }
 

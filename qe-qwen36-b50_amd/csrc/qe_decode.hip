@@ -110,14 +110,18 @@ QE_DEV float tv_val(uint64_t w) { return __uint_as_float((unsigned)w); }
 // Bounded polling: after pc.cap failed reads a poll gives up, records the
 // launch in the host-visible error word (system scope: the host reads it
 // without synchronising the stream) and goes on with what it read, so every
-// wave still reaches the end of the kernel.
+// wave still reaches the end of the kernel.  A wave whose poll gave up makes
+// every later poll of the launch with a cap of QE_DECODE_SPIN_CAP_LATE reads:
+// the launch is already invalid, and it should end soon rather than wait the
+// full cap once per poll (tens of minutes over 40 layers).
 struct PollCtl {
     unsigned *err;  // host-mapped word: 0, or 1 + the epoch of a launch whose poll timed out
-    int cap;        // reads a poll makes before it gives up
+    int cap;        // reads a poll makes before it gives up (per wave; lowered after a timeout)
     unsigned val;   // what this launch records
 };
-QE_DEV void poll_timeout(const PollCtl &pc) {
+QE_DEV void poll_timeout(PollCtl &pc) {
     __hip_atomic_store(pc.err, pc.val, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    pc.cap = pc.cap < QE_DECODE_SPIN_CAP_LATE ? pc.cap : QE_DECODE_SPIN_CAP_LATE;
 }
 
 // Read N tagged words w[i] = src[i * stride] until every one carries `tag`
@@ -126,7 +130,7 @@ QE_DEV void poll_timeout(const PollCtl &pc) {
 // reads per poller, the extra polling traffic delayed the producers' stores
 // more than it shortened detection (1,680 vs 1,620 / 1,551 / 1,494 tokens/s).
 template <int N>
-QE_DEV void read_tv(const uint64_t *src, int stride, unsigned tag, uint64_t w[N], bool act, const PollCtl &pc) {
+QE_DEV void read_tv(const uint64_t *src, int stride, unsigned tag, uint64_t w[N], bool act, PollCtl &pc) {
     for (int spins = 0;; ++spins) {
         unsigned bad = 0;
 #pragma unroll
@@ -240,7 +244,7 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
     }
     __syncthreads();
     const unsigned epoch = (unsigned)s_misc[1];
-    const PollCtl pc{a.err, a.spin_cap, 1u + (epoch & 0x7fffffffu)};
+    PollCtl pc{a.err, a.spin_cap, 1u + (epoch & 0x7fffffffu)};
     uint64_t *EX = a.ex;                                   // replica 0 (writes go to all REP)
     const uint64_t *EXr = a.ex + (size_t)(blockIdx.x % REP) * EX_TOTAL; // the copy this workgroup reads
     constexpr bool mode16 = TM == 1; // 16-row units, fp32 h (one token: 8 items x 32 units fill the grid)
@@ -330,8 +334,13 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
             read_tv<4>(src_xs + t * 256 + 4 * lane, 1, tagIn, w, true, pc);
             const float ss = wave_sum_canon((tv_val(w[0]) + tv_val(w[1])) + (tv_val(w[2]) + tv_val(w[3])));
             if (lane == 0) s_inv[t] = 1.0f / sqrtf(ss / (float)QE_D + QE_RMS_EPS);
-            if (TM == 1 && lane == 0) // 1/rms, and post_norm (this wave's loads into LDS, waited for by the poll), are in place
-                __hip_atomic_store(&s_misc[3], (int)tagIn, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+            if (TM == 1) {
+                // 1/rms and post_norm are in place: post_norm came by global->LDS loads of
+                // this wave, which complete into LDS only as vmcnt drains, and a
+                // workgroup-scope release does not wait for vmcnt
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                if (lane == 0) __hip_atomic_store(&s_misc[3], (int)tagIn, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+            }
         }
         // raw x of all tokens -> LDS (natural layout, token stride 2048; T*2048 = 2 T NTH)
         if (li == 0) {
@@ -1000,6 +1009,10 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
                         for (int r = 0; r < REP; ++r) ST_A(dst_x + r * EX_TOTAL + ro, pack_tv(out, tagD));
                         float *s_gx = (float *)(lds + L_GX);
                         s_gx[k] = out;
+                        // the 8 rows' stores (lanes of wave 0) before lane 0 reads them
+                        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                        __builtin_amdgcn_wave_barrier();
+                        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
                         if (k == 0) {
                             const float g = sumsq_group8(s_gx);
 #pragma unroll
@@ -1094,6 +1107,9 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
                         // these threads are all in wave 0, whose LDS accesses are ordered
                         float *s_gx = (float *)(lds + L_GX);
                         s_gx[t * 8 + k] = out;
+                        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                        __builtin_amdgcn_wave_barrier();
+                        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
                         if (k == 0) {
                             const float g = sumsq_group8(s_gx + t * 8);
 #pragma unroll

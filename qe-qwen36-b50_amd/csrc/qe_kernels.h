@@ -97,6 +97,7 @@ hipError_t qe_launch_decode(const QeDecodeArgs &a, hipStream_t st);
                    8 * QE_FF_EXP + 2 * QE_SMALL_T * 256))
 #define QE_DECODE_SYNC_WORDS 64 /* launch epoch, exit counter */
 #define QE_DECODE_SPIN_CAP (1 << 22) /* poll reads (s_sleep 1 between) before an exchange wait gives up */
+#define QE_DECODE_SPIN_CAP_LATE 16  /* the cap of a wave's polls after one of them gave up */
 
 // Launchers (qe_kernels.hip).  xin: layer input; post_norm: nullptr = input is
 // already normalised; x2: residual added to the output or nullptr.
@@ -108,6 +109,8 @@ hipError_t qe_launch_dispatch(const QeScratch &S, int T, hipStream_t st);
 // off and pairs are the caller's device buffers.
 #define QE_DISPATCH_NOALLOC_T_MAX 16384
 hipError_t qe_launch_dispatch_noalloc(const int32_t *ids, int T, int32_t *off, int32_t *pairs, hipStream_t st);
+// the current device's address of that array, looked up once per device
+hipError_t qe_noalloc_prepare(uint8_t **base);
 hipError_t qe_launch_expert_mfma(const QeLayerPtrs &L, const QeScratch &S, int T, hipStream_t st);
 hipError_t qe_launch_router_shgu(const QeLayerPtrs &L, const QeScratch &S, int T, hipStream_t st);
 

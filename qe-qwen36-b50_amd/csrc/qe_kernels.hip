@@ -395,22 +395,31 @@ static __device__ __align__(256) uint8_t scratch[NOALLOC_BYTES];
 static std::mutex g_noalloc_mu;
 static void *g_noalloc_ptr[NOALLOC_MAX_DEV];
 
-hipError_t qe_launch_dispatch_noalloc(const int32_t *ids, int T, int32_t *off, int32_t *pairs, hipStream_t st) {
-    if (T < 1 || T > QE_DISPATCH_NOALLOC_T_MAX) return hipErrorInvalidValue;
+// Looks up the current device's copy of `scratch` once.  qe_moe_create calls it
+// for its device, so a caller holding a context can capture the no-allocation
+// dispatch into a graph from its first call (the lookup may load the code
+// object, which a capturing stream must not see); without a context, the first
+// call on a device does the lookup and has to run before any capture.
+hipError_t qe_noalloc_prepare(uint8_t **base) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return e;
     if (dev < 0 || dev >= NOALLOC_MAX_DEV) return hipErrorInvalidDevice;
-    uint8_t *base;
-    {
-        std::lock_guard<std::mutex> lk(g_noalloc_mu);
-        if (!g_noalloc_ptr[dev]) {
-            void *p = nullptr;
-            if ((e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch))) != hipSuccess) return e;
-            g_noalloc_ptr[dev] = p;
-        }
-        base = (uint8_t *)g_noalloc_ptr[dev];
+    std::lock_guard<std::mutex> lk(g_noalloc_mu);
+    if (!g_noalloc_ptr[dev]) {
+        void *p = nullptr;
+        if ((e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch))) != hipSuccess) return e;
+        g_noalloc_ptr[dev] = p;
     }
+    if (base) *base = (uint8_t *)g_noalloc_ptr[dev];
+    return hipSuccess;
+}
+
+hipError_t qe_launch_dispatch_noalloc(const int32_t *ids, int T, int32_t *off, int32_t *pairs, hipStream_t st) {
+    if (T < 1 || T > QE_DISPATCH_NOALLOC_T_MAX) return hipErrorInvalidValue;
+    uint8_t *base = nullptr;
+    const hipError_t e = qe_noalloc_prepare(&base);
+    if (e != hipSuccess) return e;
     int32_t *chunk_hist = (int32_t *)base;
     int4 *items = (int4 *)(base + NOALLOC_HIST_BYTES);
     int32_t *n_items = (int32_t *)(base + NOALLOC_HIST_BYTES + (size_t)NOALLOC_ITEMS * 16);

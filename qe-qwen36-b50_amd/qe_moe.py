@@ -36,6 +36,7 @@ NPROF = 11
 SRC_F32, SRC_F16, SRC_Q8_0, SRC_BF16 = 0, 1, 8, 30
 QE_OK, QE_ERR_ARG, QE_ERR_HIP, QE_ERR_OOM, QE_ERR_STATE = 0, -1, -2, -3, -4
 QE_MOE_DISPATCH_NOALLOC_T_MAX = 16384  # include/qe_moe.h
+QE_MOE_T_MAX = 65536  # include/qe_moe.h: the largest t_max of a context
 
 
 class LibraryMissing(RuntimeError):

@@ -35,6 +35,15 @@ def test_expert_bytes_and_argument_errors():
     assert lib.qe_moe_convert_experts(None, 0, 16, 32, 48, 8, None) == qe_moe.QE_ERR_ARG
 
 
+def test_python_constants_match_the_header():
+    import os
+    import re
+    hdr = open(qe_moe.HEADER).read()
+    for name in ("QE_MOE_T_MAX", "QE_MOE_DISPATCH_NOALLOC_T_MAX"):
+        assert int(re.search(r"#define %s (\d+)" % name, hdr).group(1)) == getattr(qe_moe, name), name
+    assert os.path.exists(qe_moe.HEADER)
+
+
 def test_missing_library_fails_loudly(tmp_path):
     saved = qe_moe._lib
     qe_moe._lib = None

@@ -183,6 +183,40 @@ def test_cfg4_prefill_8192_skewed(ctx, torch_cuda):
     say(f"  distinct {np.count_nonzero(cnt)}, max/expert {cnt.max()}, <4 tokens {int(((cnt > 0) & (cnt < 4)).sum())}")
 
 
+def test_prefill_at_abi_max_T(torch_cuda):
+    """T = QE_MOE_T_MAX (65,536 tokens, 524,288 pairs), the largest call the ABI
+    accepts, with config 4's Zipf s=1.3 bias: logits, ids, offsets and the
+    permutation on every token, outputs on a sample (the oracle's full layer at
+    this T would take many minutes on the host)."""
+    torch = torch_cuda
+    T = qe_moe.QE_MOE_T_MAX
+    m = qe_moe.MoE(n_layers=1, t_max=T)
+    try:
+        say(f"prefill at the ABI maximum: T={T}, Zipf s=1.3")
+        L = O.SynthLayer(SEED, 0, bias=O.gen_zipf_bias(SEED, 0, 1.3))
+        m.synth_layer(0, SEED, L.bias)
+        x = O.gen_x(SEED, 65, T)
+        xd = torch.from_numpy(x).cuda()
+        y = torch.empty_like(xd)
+        m.forward_normed(0, xd, y, T)
+        torch.cuda.synchronize()
+        g = m.routing(T)
+        g["logits"] = m.logits(T)
+        g["out"] = y.cpu().numpy()
+        lg = O.router(x, L.router, L.bias)
+        assert np.array_equal(g["logits"].view(np.uint32), lg.view(np.uint32)), "router logits differ"
+        ids, _, _ = O.topk(lg)
+        assert np.array_equal(g["ids"], ids), "routing ids differ"
+        off, pairs = O.dispatch(ids)
+        assert np.array_equal(g["off"], off) and np.array_equal(g["pairs"], pairs), "dispatch differs"
+        sample = np.sort(np.random.default_rng(65).choice(T, 64, replace=False))
+        check_layer(L, g, x, sample=sample)
+        cnt = np.diff(off)
+        say(f"  distinct {np.count_nonzero(cnt)}, max/expert {cnt.max()}, <4 tokens {int(((cnt > 0) & (cnt < 4)).sum())}")
+    finally:
+        m.close()
+
+
 @pytest.mark.parametrize("T,norm", [(33, False), (100, True), (257, False), (2085, True), (4133, False)])
 def test_prefill_ragged_T(ctx, torch_cuda, T, norm):
     # T off the 32-token shared-expert tiles and the 64-token router tiles; the

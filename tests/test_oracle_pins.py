@@ -141,6 +141,24 @@ def test_dot_nl4_brute_force_and_forms_agree():
     assert not np.array_equal(wrong, _decode_nl4_row(row, 512)[0])
 
 
+def test_dot_nl4_x4_equals_single_token_dots():
+    # the CPU baseline's 4-token form (weights decoded once per group, the
+    # reference's cpu_dot_nl4_x4) gives each token the single-token result bit
+    # for bit, for every group size 1..4 and both row lengths; a per-group
+    # scale slip (token 0's xs used for all) must not pass
+    rng = np.random.default_rng(41)
+    blob = O.gen_expert(SEED, 1, 7)
+    for cols, off, rb in ((2048, 5 * 1152, 1152), (512, 1179648 + 1000 * 288, 288)):
+        row = blob[off: off + rb]
+        xq, xs = zip(*[O.quant_x(rng.standard_normal(cols).astype(np.float32) * (1 + 3 * i)) for i in range(4)])
+        for n in range(1, 5):
+            got = O.dot_nl4_x4(row, cols, xq[:n], xs[:n])
+            want = np.array([O.dot_nl4(row, cols, xq[i], xs[i], avx2=True) for i in range(n)], np.float32)
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (cols, n)
+        slip = O.dot_nl4_x4(row, cols, xq, [xs[0]] * 4)
+        assert not np.array_equal(slip[1:].view(np.uint32), want[1:].view(np.uint32))
+
+
 def test_canon_dot_and_rmsnorm():
     rng = np.random.default_rng(5)
     a = rng.standard_normal(2048).astype(np.float32)
