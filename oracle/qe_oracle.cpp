@@ -188,6 +188,10 @@ ORC_API void orc_dot_nl4_x4_avx2(const uint8_t *row, int cols, const int8_t *con
     const __m128i tbl = _mm_loadu_si128((const __m128i *)QE_KVALUES_NL4);
     const __m128i m4 = _mm_set1_epi8(0x0f);
     const __m256i ones = _mm256_set1_epi16(1);
+    if (n == 1) { // one token (the reference's B = 1 decode pool calls cpu_dot_nl4 itself, :777-778)
+        out[0] = orc_dot_nl4_avx2(row, cols, xq[0], xs[0]);
+        return;
+    }
     __m256 acc[4];
     for (int t = 0; t < 4; ++t) acc[t] = _mm256_setzero_ps();
     for (int b = 0; b < cols / 32; ++b) {
