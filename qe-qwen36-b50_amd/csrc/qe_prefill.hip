@@ -18,6 +18,11 @@
 
 typedef _Float16 qe_half8 __attribute__((ext_vector_type(8)));
 
+// int32 -> fp32 without a conversion: the float with bits 0x4B400000 + P is
+// 3 * 2^22 + P exactly for |P| < 2^22 (the binade [2^23, 2^24) has ulp 1).
+#define QE_I2F_MAGIC_BITS 0x4B400000
+#define QE_I2F_MAGIC 12582912.0f
+
 
 // fp16 of small integers: half(0x6400 | u) = 1024 + u for u in 0..1023, so a
 // biased byte u = v + 128 becomes v exactly after subtracting 1152.
@@ -283,13 +288,21 @@ __device__ __forceinline__ void expert_tile(const GemmTileArgs &a, const int4 it
                     // tokens, -6 % at 8192)
                     typedef _Float16 hNC __attribute__((ext_vector_type(NC)));
                     const hNC dw = *(const hNC *)(lds + LY::DW + (((8 * ch + s) * 4 + wv) * 16 + n) * NC * 2);
-                    float dwf[NC];
+                    // dwf = dw, cng = -QE_I2F_MAGIC * dw: exact in fp32 (dw has at most 11
+                    // significant bits, 3 dw at most 13, and QE_I2F_MAGIC = 3 * 2^22)
+                    float dwf[NC], cng[NC];
 #pragma unroll
                     for (int c = 0; c < NC; ++c) {
                         dwf[c] = (float)dw[c];
-                        asm volatile("" : "+v"(dwf[c]));
+                        cng[c] = dwf[c] * -QE_I2F_MAGIC;
+                        asm volatile("" : "+v"(dwf[c]), "+v"(cng[c]));
                     }
-                    // per tile: NC exact block dots on the matrix cores, then the fp32 scaling
+                    // per tile: NC exact block dots on the matrix cores, each accumulated onto
+                    // the bits of QE_I2F_MAGIC, so that read as a float it is QE_I2F_MAGIC + P
+                    // exactly (|P| <= 32 * 127 * 127 < 2^22); then fma(D, dw, -QE_I2F_MAGIC dw)
+                    // = P * dw with one rounding, and one fma more with the activation scale
+                    // (two full-rate fmas per output instead of a conversion, a product and an
+                    // fma)
 #pragma unroll
                     for (int t = 0; t < NT; ++t) {
                         const uint4 v = av2[t];
@@ -298,16 +311,16 @@ __device__ __forceinline__ void expert_tile(const GemmTileArgs &a, const int4 it
                         i32x4 P[NC];
 #pragma unroll
                         for (int c = 0; c < NC; ++c) {
-                            const i32x4 zero = {0, 0, 0, 0};
-                            P[c] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bv[c], zero, 0, 0, 0);
+                            const i32x4 mag = {QE_I2F_MAGIC_BITS, QE_I2F_MAGIC_BITS, QE_I2F_MAGIC_BITS, QE_I2F_MAGIC_BITS};
+                            P[c] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bv[c], mag, 0, 0, 0);
                         }
                         const float4 x4 = *(const float4 *)(xsl + s * 16 * NT + 16 * t + 4 * g);
 #pragma unroll
                         for (int c = 0; c < NC; ++c) {
-                            acc[c][t][0] = fmaf((float)P[c][0], x4.x * dwf[c], acc[c][t][0]);
-                            acc[c][t][1] = fmaf((float)P[c][1], x4.y * dwf[c], acc[c][t][1]);
-                            acc[c][t][2] = fmaf((float)P[c][2], x4.z * dwf[c], acc[c][t][2]);
-                            acc[c][t][3] = fmaf((float)P[c][3], x4.w * dwf[c], acc[c][t][3]);
+                            acc[c][t][0] = fmaf(fmaf(__int_as_float(P[c][0]), dwf[c], cng[c]), x4.x, acc[c][t][0]);
+                            acc[c][t][1] = fmaf(fmaf(__int_as_float(P[c][1]), dwf[c], cng[c]), x4.y, acc[c][t][1]);
+                            acc[c][t][2] = fmaf(fmaf(__int_as_float(P[c][2]), dwf[c], cng[c]), x4.z, acc[c][t][2]);
+                            acc[c][t][3] = fmaf(fmaf(__int_as_float(P[c][3]), dwf[c], cng[c]), x4.w, acc[c][t][3]);
                         }
                     }
                     // scale now: left alone the compiler defers the block's scaling,
