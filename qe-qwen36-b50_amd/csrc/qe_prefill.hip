@@ -60,6 +60,7 @@ struct GemmTileArgs {
     const float *wts;          // pair weights (down)
     int8_t *hq; float *hs;     // gate/up output: quantised h (operand layout) + block scales
     float *yp;                 // down output
+    int dn_rgw;                // down: row groups of 128 output rows per workgroup (1, 2 or 4)
 };
 
 // v_mfma_i32_16x16x32_i8 with one 32-element block per instruction keeps the
@@ -878,23 +879,222 @@ QE_DEV void shdn_tile64(const _Float16 *hhl, int T, const uint8_t *W, float *out
     }
 }
 
+// Routed down of one item over nrg row groups of 128 output rows.  K is only
+// 16 blocks, so the item's whole h (up to 64 pairs x 512 int8 in the operand
+// layout, 32 KB) and its block scales are staged in LDS once, and each wave then
+// streams its 32 rows (two 16-row column groups) of every row group through the
+// code ring with no further barrier: one staging of the activations and one
+// start-up for 128 nrg rows, where a workgroup per row group paid both per 128.
+// The code ring holds two quads (4 blocks each) of both column groups, and
+// with them the quad's four weight scales; quad qi is blocks 4 (qi % 4) .. + 3
+// of row group rg0 + qi / 4, refilled two quads ahead (the last refills read
+// the last quad again).  Arithmetic as expert_tile: exact int8 block dots
+// accumulated onto QE_I2F_MAGIC, two fmas per output and block.
+struct DnSmem {
+    alignas(16) uint8_t act[QE_MFMA_MC * QE_FF_EXP]; // [pair][512 B], 16-byte chunk q of pair m at q ^ (m % 16)
+    float xs[QE_FF_EXP / 32][QE_MFMA_MC];           // [block][pair] activation block scales
+    float w[QE_MFMA_MC];                            // pair weights
+    int pair[QE_MFMA_MC];
+};
+template <int NT>
+__device__ __forceinline__ void dn_tile(const GemmTileArgs &a, const int4 it, const int rg0, const int nrg, DnSmem &sm) {
+    constexpr int NC = 2;
+    constexpr uint32_t RB = QE_DN_ROW_BYTES;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, n = lane & 15, g = lane >> 4;
+    const uint8_t *dbase = a.arena + (size_t)it.x * QE_EXPERT_BYTES + QE_EXPERT_DOWN_OFF;
+    const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)dbase, (short)0, (int)(QE_EXPERT_BYTES - QE_EXPERT_DOWN_OFF), 0x00020000);
+    const __amdgpu_buffer_rsrc_t ar = __builtin_amdgcn_make_buffer_rsrc((void *)a.aq, (short)0, a.a_bytes, 0x00020000);
+    const int nq = 4 * nrg;
+    uint4 rq[2][NC]; // codes: lane (n, g) holds block 4 Q + g of its row
+    uint2 rs[2][NC]; // the quad's four fp16 weight scales of the lane's row
+    auto load_quad = [&](int qi, int slot, uint32_t dep) {
+        qi = qi < nq ? qi : nq - 1;
+        const int Q = qi & 3;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            const uint32_t row = (uint32_t)(128 * (rg0 + (qi >> 2)) + 32 * wv + 16 * c + n) * RB + dep;
+            const qe_u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(wr, row + 16 * g, 64 * Q, 0);
+            rq[slot][c] = make_uint4(v.x, v.y, v.z, v.w);
+            const qe_u32x2 sv = __builtin_amdgcn_raw_buffer_load_b64(wr, row + QE_FF_EXP / 2, 8 * Q, 0);
+            rs[slot][c] = make_uint2(sv.x, sv.y);
+        }
+    };
+    load_quad(0, 0, 0);
+    load_quad(1, 1, 0);
+    if (tid < QE_MFMA_MC) {
+        const int p = tid < it.z ? a.pairs[it.y + tid] : -1;
+        sm.pair[tid] = p;
+        sm.w[tid] = p >= 0 ? a.wts[p] : 0.f;
+    }
+    __syncthreads();
+    {   // activations: thread (pair (tid / 16) + 16 r, chunks (tid % 16) + 16 h); scales: (pair tid / 4, blocks 4 (tid % 4) + 0..3)
+        uint4 v[NT][2];
+#pragma unroll
+        for (int r = 0; r < NT; ++r) {
+            const int m = (tid >> 4) + 16 * r, pm = sm.pair[m];
+            const uint32_t src = (uint32_t)(pm < 0 ? sm.pair[0] : pm) * QE_FF_EXP + 16 * (tid & 15);
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const qe_u32x4 t4 = __builtin_amdgcn_raw_buffer_load_b128(ar, src, 256 * h, 0);
+                v[r][h] = make_uint4(t4.x, t4.y, t4.z, t4.w);
+            }
+        }
+        float4 sc = make_float4(0.f, 0.f, 0.f, 0.f);
+        const bool sc_role = tid < 64 * NT;
+        const int sm_m = tid >> 2;
+        if (sc_role) {
+            const int pm = sm.pair[sm_m];
+            if (pm >= 0) sc = ((const float4 *)(a.as + (size_t)pm * (QE_FF_EXP / 32)))[tid & 3];
+        }
+#pragma unroll
+        for (int r = 0; r < NT; ++r) {
+            const int m = (tid >> 4) + 16 * r;
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+                *(uint4 *)(sm.act + m * QE_FF_EXP + ((((tid & 15) + 16 * h) ^ (m & 15)) << 4)) = v[r][h];
+        }
+        if (sc_role) {
+            const int b0 = 4 * (tid & 3);
+            sm.xs[b0][sm_m] = sc.x;
+            sm.xs[b0 + 1][sm_m] = sc.y;
+            sm.xs[b0 + 2][sm_m] = sc.z;
+            sm.xs[b0 + 3][sm_m] = sc.w;
+        }
+    }
+    __syncthreads();
+
+    float acc[NC][NT][4];
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[c][t][i] = 0.f;
+    auto quad = [&](int qi, int slot) {
+        uint32_t cw[NC][4], sw[NC][2];
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            // out of the ring first: the swaps overwrite their operands, and the
+            // ring registers must stay free for the refill
+            const uint32_t r4[4] = {rq[slot][c].x, rq[slot][c].y, rq[slot][c].z, rq[slot][c].w};
+#pragma unroll
+            for (int k = 0; k < 4; ++k) asm volatile("v_mov_b32 %0, %1" : "=v"(cw[c][k]) : "v"(r4[k]));
+            asm volatile("v_mov_b32 %0, %1" : "=v"(sw[c][0]) : "v"(rs[slot][c].x));
+            asm volatile("v_mov_b32 %0, %1" : "=v"(sw[c][1]) : "v"(rs[slot][c].y));
+            transpose_rows4(cw[c]);
+        }
+        {
+            uint32_t dep;
+            asm volatile("v_mov_b32 %0, 0" : "=v"(dep) : "v"(cw[0][0]), "v"(cw[1][0]), "v"(sw[0][0]), "v"(sw[1][0]));
+            load_quad(qi + 2, slot, dep);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        const int Q = qi & 3;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int b = 4 * Q + k;
+            long bv[NC];
+            float dwf[NC], cng[NC];
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+                uint32_t lo, hi;
+                nl4_decode_dword<true>(cw[c][k], lo, hi);
+                bv[c] = (long)(((uint64_t)hi << 32) | lo);
+                const uint32_t hw = sw[c][k >> 1] >> (16 * (k & 1));
+                dwf[c] = f16_bits_to_f32((uint16_t)hw);
+                cng[c] = dwf[c] * -QE_I2F_MAGIC;
+                asm volatile("" : "+v"(dwf[c]), "+v"(cng[c]));
+            }
+            const int cho = (((b >> 1) * 4 + g) ^ n) << 4; // the lane's 16-byte chunk of block pair b / 2
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                const long av = *(const long *)(sm.act + (16 * t + n) * QE_FF_EXP + cho + 8 * (b & 1));
+                typedef int i32x4 __attribute__((ext_vector_type(4)));
+                i32x4 P[NC];
+#pragma unroll
+                for (int c = 0; c < NC; ++c) {
+                    const i32x4 mag = {QE_I2F_MAGIC_BITS, QE_I2F_MAGIC_BITS, QE_I2F_MAGIC_BITS, QE_I2F_MAGIC_BITS};
+                    P[c] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bv[c], mag, 0, 0, 0);
+                }
+                const float4 x4 = *(const float4 *)&sm.xs[b][16 * t + 4 * g];
+#pragma unroll
+                for (int c = 0; c < NC; ++c) {
+                    acc[c][t][0] = fmaf(fmaf(__int_as_float(P[c][0]), dwf[c], cng[c]), x4.x, acc[c][t][0]);
+                    acc[c][t][1] = fmaf(fmaf(__int_as_float(P[c][1]), dwf[c], cng[c]), x4.y, acc[c][t][1]);
+                    acc[c][t][2] = fmaf(fmaf(__int_as_float(P[c][2]), dwf[c], cng[c]), x4.z, acc[c][t][2]);
+                    acc[c][t][3] = fmaf(fmaf(__int_as_float(P[c][3]), dwf[c], cng[c]), x4.w, acc[c][t][3]);
+                }
+            }
+            // scale now: left alone the compiler defers the block's scaling,
+            // keeping every block product live
+#pragma unroll
+            for (int c = 0; c < NC; ++c)
+#pragma unroll
+                for (int t = 0; t < NT; ++t)
+                    asm volatile("" : "+v"(acc[c][t][0]), "+v"(acc[c][t][1]), "+v"(acc[c][t][2]), "+v"(acc[c][t][3]));
+        }
+        if (Q == 3) { // the row group is complete: yp[p][row] = w_p * y, accumulators cleared
+            const int rg = rg0 + (qi >> 2);
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int m = 16 * t + 4 * g + i, pm = sm.pair[m];
+                    if (pm >= 0) {
+                        const float w = sm.w[m];
+                        float *yrow = a.yp + (size_t)pm * QE_D + 128 * rg + 32 * wv + n;
+#pragma unroll
+                        for (int c = 0; c < NC; ++c) yrow[16 * c] = w * acc[c][t][i];
+                    }
+#pragma unroll
+                    for (int c = 0; c < NC; ++c) acc[c][t][i] = 0.f;
+                }
+        }
+    };
+    for (int qi = 0; qi < nq; qi += 2) {
+        quad(qi, 0);
+        quad(qi + 1, 1);
+    }
+}
+
+// Down workgroup b: item and row-group block; all row-group blocks of an item
+// on one XCD (b % 8), as for gate/up.  Big items run NT = 4, smaller NT = 2, 1.
+__device__ __forceinline__ void dn_unit(const GemmTileArgs &a, int b, DnSmem &sm) {
+    const int rgb_n = (QE_D / 128) / a.dn_rgw; // row-group blocks per item
+    const int k = b >> 3, item = (k / rgb_n) * 8 + (b & 7), rgb = k % rgb_n;
+    if (item >= a.n_items[0]) return;
+    const int4 it = a.items[item];
+    static_assert(QE_MFMA_MC == 64, "items of up to four 16-row tiles");
+    if (it.z > 32)
+        dn_tile<4>(a, it, rgb * a.dn_rgw, a.dn_rgw, sm);
+    else if (it.z > 16)
+        dn_tile<2>(a, it, rgb * a.dn_rgw, a.dn_rgw, sm);
+    else
+        dn_tile<1>(a, it, rgb * a.dn_rgw, a.dn_rgw, sm);
+}
+// workgroups of the routed down over the items of np pairs (as expert_max_wg)
+QE_HD int dn_max_wg(int np, int rgw) { return ((QE_D / 128) / rgw) * (((np / (QE_MFMA_MC / 2 + 1) + 1 + QE_N_EXPERT) + 7) & ~7); }
+
 // Routed down items and shared down tiles in one launch: the routed items
-// (item, then row group) come first, the shared tiles fill the CUs as the
+// (item, then row-group block) come first, the shared tiles fill the CUs as the
 // routed work drains.
 __global__ __launch_bounds__(256, 2) void k_expert_dn(GemmTileArgs a, int nr, const _Float16 *hhl, int T,
                                                       const uint8_t *Wsd, float *sd) {
-    __shared__ ExpertSmem<false> sm;
+    __shared__ union {
+        DnSmem d;
+        Shdn64Lds s;
+    } sm;
     const int b = blockIdx.x;
     if (b < nr) {
-        expert_unit<false>(a, b, sm);
+        dn_unit(a, b, sm.d);
     } else {
         const int s = b - nr;
         // tile s runs on XCD s % 8 (nr is a multiple of 8 below): the 16 column
         // tiles of one 64-token pair back to back there
         const int x = s & 7, k = s >> 3, mp = 8 * (k / (QE_D / 128)) + x;
         if (mp >= (T + 63) / 64) return;
-        static_assert(sizeof(Shdn64Lds) <= sizeof(sm.raw), "shared down staging fits the down tile's LDS");
-        shdn_tile64(hhl, T, Wsd, sd, mp, k % (QE_D / 128), sm.raw);
+        shdn_tile64(hhl, T, Wsd, sd, mp, k % (QE_D / 128), (uint8_t *)&sm.s);
     }
 }
 
@@ -909,6 +1109,12 @@ hipError_t qe_launch_router_shgu(const QeLayerPtrs &L, const QeScratch &S, int T
     return hipGetLastError();
 }
 
+#ifndef QE_DN_RGW4_T
+#define QE_DN_RGW4_T 256
+#endif
+#ifndef QE_DN_RGW2_T
+#define QE_DN_RGW2_T 256
+#endif
 hipError_t qe_launch_expert_mfma(const QeLayerPtrs &L, const QeScratch &S, int T, hipStream_t st) {
     const int np = T * QE_K_USED;
     GemmTileArgs g{};
@@ -916,8 +1122,11 @@ hipError_t qe_launch_expert_mfma(const QeLayerPtrs &L, const QeScratch &S, int T
     g.aq = S.xqp; g.a_bytes = T * QE_D; g.as = S.xs; g.a_row_div = QE_K_USED; g.hq = S.hqp; g.hs = S.hs;
     k_expert_gu<<<expert_max_wg<true>(np), 256, 0, st>>>(g);
     g.aq = S.hqp; g.a_bytes = np * QE_FF_EXP; g.as = S.hs; g.a_row_div = 1; g.yp = S.yp;
+    // row groups per down workgroup: fewer, longer workgroups where the items
+    // alone fill the CUs several times over
+    g.dn_rgw = T >= QE_DN_RGW4_T ? 4 : T >= QE_DN_RGW2_T ? 2 : 1; // 4 from 256 tokens: measured best at 512 and 8192
     const int nsh = 8 * (QE_D / 128) * (((T + 63) / 64 + 7) / 8);
-    const int nr = expert_max_wg<false>(np); // a multiple of 8: shared tiles start on XCD 0
+    const int nr = dn_max_wg(np, g.dn_rgw); // a multiple of 8: shared tiles start on XCD 0
     k_expert_dn<<<nr + nsh, 256, 0, st>>>(g, nr, (const _Float16 *)S.shgu, T, L.sh_dn, S.sd);
     return hipGetLastError();
 }
