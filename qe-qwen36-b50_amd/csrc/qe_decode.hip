@@ -144,6 +144,31 @@ QE_DEV void read_tv(const uint64_t *src, int stride, unsigned tag, uint64_t w[N]
     }
 }
 
+// The same poll for N = 2 M consecutive words (16-byte aligned), read two per
+// 16-byte load: each word carries its own tag, and an aligned 8-byte word is
+// never torn, so a load that catches one half written and the other not simply
+// polls again.  Half the requests of M pairs of 8-byte polls.
+typedef unsigned qe_dec_u32x4 __attribute__((ext_vector_type(4)));
+template <int M>
+QE_DEV void read_tv_pairs(const uint64_t *src, unsigned tag, uint64_t w[2 * M], PollCtl &pc) {
+    for (int spins = 0;; ++spins) {
+        unsigned bad = 0;
+        qe_dec_u32x4 v[M];
+#pragma unroll
+        for (int i = 0; i < M; ++i) asm volatile("global_load_dwordx4 %0, %1, off sc1" : "=v"(v[i]) : "v"(src + 2 * i) : "memory");
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+        for (int i = 0; i < M; ++i) {
+            w[2 * i] = ((uint64_t)v[i].y << 32) | v[i].x;
+            w[2 * i + 1] = ((uint64_t)v[i].w << 32) | v[i].z;
+            bad |= (v[i].y ^ tag) | (v[i].w ^ tag);
+        }
+        if (__all(bad == 0)) break;
+        if (spins + 1 >= pc.cap) { poll_timeout(pc); break; }
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
+
 // Gate/up rows of one unit: this lane's NB blocks of its row (blocks c + LPR i,
 // LPR = 64 / NB lanes per row), dotted with the int8 x of every pair of the item;
 // the row total lands in s_gu[row_in_unit * 8 + pair].
@@ -331,7 +356,7 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
         if (li > 0 && wv < T) {
             const int t = wv;
             uint64_t w[4];
-            read_tv<4>(src_xs + t * 256 + 4 * lane, 1, tagIn, w, true, pc);
+            read_tv_pairs<2>(src_xs + t * 256 + 4 * lane, tagIn, w, pc);
             const float ss = wave_sum_canon((tv_val(w[0]) + tv_val(w[1])) + (tv_val(w[2]) + tv_val(w[3])));
             if (lane == 0) s_inv[t] = 1.0f / sqrtf(ss / (float)QE_D + QE_RMS_EPS);
             if (TM == 1) {
@@ -364,8 +389,8 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
         } else if (TM == 1 || T <= 2) {
             for (int i0 = 0; i0 < T * QE_D; i0 += 2 * NTH) {
                 uint64_t w[2];
-                read_tv<2>(src_x + i0 + tid, NTH, tagIn, w, true, pc);
-                const int e0 = i0 + tid, e1 = e0 + NTH;
+                read_tv_pairs<1>(src_x + i0 + 2 * tid, tagIn, w, pc);
+                const int e0 = i0 + 2 * tid, e1 = e0 + 1;
                 float x0 = tv_val(w[0]), x1 = tv_val(w[1]);
                 if (TM == 1 && pnorm) { // scaled as it arrives, once wave 0 has 1/rms
                     while (__hip_atomic_load(&s_misc[3], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) != (int)tagIn) {
@@ -948,7 +973,7 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
             const int u = wv >> 1, hw = wv & 1, b = 8 * hw + (lane & 7);
             static_assert(8 * QE_FF_EXP == 4 * NTH, "h of the 8 pairs: four words per thread");
             uint64_t w[4];
-            read_tv<4>(EXr + EX_HF + 4 * tid, 1, tagG, w, true, pc);
+            read_tv_pairs<2>(EXr + EX_HF + 4 * tid, tagG, w, pc);
             float h[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) h[i] = tv_val(w[i]);
