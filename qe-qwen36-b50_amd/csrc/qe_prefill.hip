@@ -991,9 +991,17 @@ __device__ __forceinline__ void dn_tile(const GemmTileArgs &a, const int4 it, co
             __builtin_amdgcn_sched_barrier(0);
         }
         const int Q = qi & 3;
+        uint4 av2[NT]; // 16 bytes per tile: the lane's activations of blocks b, b + 1 (b even)
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             const int b = 4 * Q + k;
+            if ((k & 1) == 0) {
+                // one 16-byte read per tile and block pair: a quarter wave (16 lanes,
+                // one lane group g) covers 16 distinct chunks, i.e. all 64 banks
+                const int cho = ((2 * Q + (k >> 1)) * 4 + g) ^ n;
+#pragma unroll
+                for (int t = 0; t < NT; ++t) av2[t] = *(const uint4 *)(sm.act + (16 * t + n) * QE_FF_EXP + (cho << 4));
+            }
             long bv[NC];
             float dwf[NC], cng[NC];
 #pragma unroll
@@ -1006,10 +1014,9 @@ __device__ __forceinline__ void dn_tile(const GemmTileArgs &a, const int4 it, co
                 cng[c] = dwf[c] * -QE_I2F_MAGIC;
                 asm volatile("" : "+v"(dwf[c]), "+v"(cng[c]));
             }
-            const int cho = (((b >> 1) * 4 + g) ^ n) << 4; // the lane's 16-byte chunk of block pair b / 2
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
-                const long av = *(const long *)(sm.act + (16 * t + n) * QE_FF_EXP + cho + 8 * (b & 1));
+                const long av = (k & 1) ? (long)(((uint64_t)av2[t].w << 32) | av2[t].z) : (long)(((uint64_t)av2[t].y << 32) | av2[t].x);
                 typedef int i32x4 __attribute__((ext_vector_type(4)));
                 i32x4 P[NC];
 #pragma unroll
