@@ -26,7 +26,12 @@ __global__ __launch_bounds__(256) void k_normq(const float *x, int T, const floa
     // stores of the rows, lane c of wave w working on elements [32c, 32c+32) of
     // row w (chunks padded to 33 words: conflict-free both ways)
     __shared__ float s_r[4][64 * 33];
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, t0 = blockIdx.x * 4, t = t0 + wv;
+    // the 8 workgroups of a 32-token tile of xhl run on one XCD (b % 8), so the
+    // tile's lines are completed in one L2: b = 64 G + 8 s + x -> tokens
+    // 32 (8 G + x) + 4 s .. + 3
+    const int b = blockIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, t0 = 32 * (8 * (b >> 6) + (b & 7)) + 4 * ((b >> 3) & 7),
+              t = t0 + wv;
     if ((int)blockIdx.x < nch) chunk_hist[blockIdx.x * QE_N_EXPERT + tid] = 0; // dispatch histogram
 #pragma unroll
     for (int i = 0; i < 8; ++i) { // row i / 2, float4 (i & 1) * 256 + tid
@@ -332,7 +337,7 @@ hipError_t qe_launch_layer(const QeLayerPtrs &L, const QeScratch &S, const float
     QeCombineArgs da{T, S.yp, S.sd, S.shg, x2, out, exit_norm, exit_xn};
     {
         QE_PROF(QP_NORMQ);
-        k_normq<<<(T + 3) / 4, 256, 0, st>>>(xin, T, pn, S.xn, S.xqp, S.xs, S.xhl, S.chunk_hist,
+        k_normq<<<64 * ((T + 255) / 256), 256, 0, st>>>(xin, T, pn, S.xn, S.xqp, S.xs, S.xhl, S.chunk_hist,
                                               (T * QE_K_USED + 1023) / 1024, L.router, S.logits);
     }
     {
