@@ -88,7 +88,8 @@ QE_DEV int xpos(int e) { return (e & 31) * 65 + (e >> 5); } // raw x element e o
                                                     //   T > 1: u64 [8][32] survivor keys per token
 #define L_LG (L_TK + 256 * 8 + 256 * 4 + 8 * 4 + 16) // f32 [T][257] the last layer's logits (routing sink)
 #define L_IORD (L_LG + DEC_T * QE_ROUTER_ROWS * 4)   // int [64] T > 1: items in unit deal order
-#define L_TOTAL (L_IORD + 64 * 4)
+#define L_TKF (L_IORD + 64 * 4)                      // u32 [256] T = 1: a survivor's ordered logit by tie key
+#define L_TOTAL (L_TKF + 256 * 4)
 static_assert(L_YG + NWV * 4 * DEC_T * 4 <= L_U_END, "D-stage LDS must fit in the union");
 static_assert(64 * 8 * 4 <= L_HQ - L_U, "G-stage LDS must fit in front of the D buffers");
 static_assert(L_TOTAL <= 160 * 1024, "LDS budget of one workgroup per CU");
@@ -610,6 +611,7 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
             uint64_t *s_sk = (uint64_t *)(lds + L_TK);           // [256] survivors' order keys
             int *s_se = (int *)(lds + L_TK + 2048);                // [256] survivors' experts
             unsigned *s_rkey = (unsigned *)(lds + L_TK + 3072);    // [8] logit keys by rank
+            unsigned *s_full = (unsigned *)(lds + L_TKF);          // [256] survivors' logit keys by tie key
             float *s_lg256 = (float *)(lds + L_TK + 3104);
             if (wv == 0) {
                 uint64_t w[5]; // the lane's four logits and (lane 0) logit 256, one poll loop
@@ -653,8 +655,10 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
                     const unsigned long long bal = __ballot(sv);
                     if (sv) {
                         const int e = lane + 64 * j, pos = S + (int)__builtin_amdgcn_mbcnt_hi((unsigned)(bal >> 32), __builtin_amdgcn_mbcnt_lo((unsigned)bal, 0u));
-                        s_sk[pos] = ((uint64_t)v[j] << 32) | (0xffffu - (unsigned)((e & 15) * 16 + (e >> 4)));
+                        const unsigned tk = (unsigned)((e & 15) * 16 + (e >> 4));
+                        s_sk[pos] = ((uint64_t)v[j] << 32) | (0xffffu - tk);
                         s_se[pos] = e;
+                        s_full[tk] = v[j];
                     }
                     S += (int)__popcll(bal);
                 }
@@ -663,11 +667,27 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
                     // trips); a key's low half holds 0xffff - tie key, so it names its expert
                     const uint64_t ki = lane < S ? s_sk[lane] : 0ull; // real keys are never 0
                     uint32_t khi = (uint32_t)(ki >> 32), klo = (uint32_t)ki;
-                    sort32_desc_u64(khi, klo, lane);
-                    if (lane < QE_K_USED) {
-                        const unsigned tk = 0xffffu - (klo & 0xffffu); // (e % 16) * 16 + e / 16
-                        s_items[lane] = make_int4((int)(((tk & 15u) << 4) | ((tk >> 4) & 15u)), lane, 1, 0);
-                        s_rkey[lane] = khi;
+                    // First on 32-bit keys {top 24 bits of the ordered value, 0xff - tie key}:
+                    // their order is the exact one wherever no two of ranks 0..8 share the top
+                    // 24 bits (every exact tie does), which one comparison with the next rank
+                    // checks; otherwise the 64-bit keys are sorted.  (An ordered finite
+                    // logit is >= 2^23, so real keys stay above the padding's 0.)
+                    uint32_t k32 = (khi & 0xffffff00u) | (klo & 0xffu);
+                    sort32_desc_u32(k32, lane);
+                    const uint32_t nx = dpp_u<0x101>(k32); // row_shl:1, the next rank
+                    if (!__any(lane < QE_K_USED && ((k32 ^ nx) >> 8) == 0u)) {
+                        if (lane < QE_K_USED) {
+                            const unsigned tk = 0xffu - (k32 & 0xffu); // (e % 16) * 16 + e / 16
+                            s_items[lane] = make_int4((int)(((tk & 15u) << 4) | ((tk >> 4) & 15u)), lane, 1, 0);
+                            s_rkey[lane] = s_full[tk];
+                        }
+                    } else {
+                        sort32_desc_u64(khi, klo, lane);
+                        if (lane < QE_K_USED) {
+                            const unsigned tk = 0xffffu - (klo & 0xffffu);
+                            s_items[lane] = make_int4((int)(((tk & 15u) << 4) | ((tk >> 4) & 15u)), lane, 1, 0);
+                            s_rkey[lane] = khi;
+                        }
                     }
                 } else {
                     for (int i0 = 0; i0 < S; i0 += 64) { // many equal logits: count the survivors ahead

@@ -201,6 +201,41 @@ QE_DEV void sort32_desc_u64(uint32_t &hi, uint32_t &lo, int lane) {
     xor1();
 }
 
+// The same network on 32-bit keys (each step a max, a min and a select).
+QE_DEV void cx32(uint32_t &k, uint32_t p, bool lower) {
+    const uint32_t mx = k > p ? k : p, mn = k > p ? p : k;
+    k = lower ? mx : mn;
+}
+QE_DEV void sort32_desc_u32(uint32_t &k, int lane) {
+    auto xor1 = [&]() { cx32(k, dpp_u<QE_DPP_XOR1>(k), !(lane & 1)); };
+    auto xor2 = [&]() { cx32(k, dpp_u<QE_DPP_XOR2>(k), !(lane & 2)); };
+    auto xor4 = [&]() {
+        const bool up = lane & 4;
+        const uint32_t r = dpp_u<0x114>(k), l = dpp_u<0x104>(k);
+        cx32(k, up ? r : l, !up);
+    };
+    xor1();                                              // k = 2
+    cx32(k, dpp_u<0x1B>(k), !(lane & 2));                // k = 4
+    xor1();
+    cx32(k, dpp_u<QE_DPP_HMIRROR>(k), !(lane & 4));      // k = 8
+    xor2();
+    xor1();
+    cx32(k, dpp_u<QE_DPP_MIRROR>(k), !(lane & 8));       // k = 16
+    xor4();
+    xor2();
+    xor1();
+    {   // k = 32
+        unsigned a, b;
+        rows16(dpp_u<QE_DPP_MIRROR>(k), a, b);
+        const bool r1 = lane & 16;
+        cx32(k, r1 ? a : b, !r1);
+    }
+    cx32(k, dpp_u<0x128>(k), !(lane & 8));
+    xor4();
+    xor2();
+    xor1();
+}
+
 QE_DEV unsigned wave_min_u32(unsigned v) {
     v = umin32(v, dpp_ub<QE_DPP_XOR1>(v));
     v = umin32(v, dpp_ub<QE_DPP_XOR2>(v));

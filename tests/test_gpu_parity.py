@@ -259,28 +259,43 @@ def test_prefill_item_boundaries(ctx, torch_cuda, T):
     assert sorted(np.flatnonzero(cnt).tolist()) == hot and set(cnt[hot].tolist()) == {T}
 
 
-def tied_layer(kind):
-    """Layer 1's synthetic weights with a router that forces equal logits."""
-    L = O.SynthLayer(SEED, 1)
+NEAR_BIAS = {0: 0.0, 1: 1e-6, 16: 2e-6, 32: 3e-6}
+
+
+def tied_layer(kind, x=None):
+    """Layer 1's synthetic weights with a router that forces equal logits (or,
+    for "near", logits a few ulps apart; the shared row is turned towards the
+    first token of x, so that the group is in that token's top 8)."""
+    bias = None
+    if kind == "near":
+        bias = np.zeros(256, np.float32)
+        for e, b in NEAR_BIAS.items():
+            bias[e] = b
+    L = O.SynthLayer(SEED, 1, bias=bias)
     R = L.router.copy()
     if kind == "zero":  # every logit 0: top-8 is the tie order itself
         R[:] = 0.0
     else:  # experts 0, 1, 16, 32 share one (scaled-up) row: ties between large logits
         R[0] *= 8.0
+        if kind == "near" and x is not None and float(np.dot(x[0].astype(np.float64), R[0])) < 0.0:
+            R[0] = -R[0]
         R[1] = R[16] = R[32] = R[0]
     L.router = np.ascontiguousarray(R, np.float32)
     return L
 
 
-@pytest.mark.parametrize("kind", ["zero", "dup"])
+@pytest.mark.parametrize("kind", ["zero", "dup", "near"])
 @pytest.mark.parametrize("T", [1, 5, 64])
 def test_topk_ties_on_gpu(ctx, torch_cuda, kind, T):
-    # ties go to the smaller (e % 16, e / 16): all-equal logits select 0, 16, ..., 112
+    # ties go to the smaller (e % 16, e / 16): all-equal logits select 0, 16, ..., 112.
+    # "near": the shared row plus biases of 0, 1, 2, 3 x 1e-6 puts the four experts'
+    # logits a few ulps apart (|logit| of a few units has ulps of 2.4e-7 .. 9.5e-7), not
+    # equal: the order must follow the values, down to the last bit
     say(f"top-8 ties ({kind} router), T={T}")
-    L = tied_layer(kind)
-    ctx.synth_layer(1, SEED, None)
-    ctx.set_dense(1, router=L.router)
     x = O.gen_x(SEED, 400 + T, T)
+    L = tied_layer(kind, x)
+    ctx.synth_layer(1, SEED, L.bias)
+    ctx.set_dense(1, router=L.router)
     xd = torch_cuda.from_numpy(x).cuda()
     y = torch_cuda.empty_like(xd)
     ctx.forward_normed(1, xd, y, T)
@@ -294,6 +309,10 @@ def test_topk_ties_on_gpu(ctx, torch_cuda, kind, T):
     else:
         tied = np.isin(o["ids"], [0, 1, 16, 32]).sum(axis=1)
         say(f"  tokens with the tied group in their top-8: {(tied == 4).sum()} of {T}")
+        if kind == "near":
+            grp = o["logits"][:, [0, 1, 16, 32]]
+            distinct = (np.diff(np.sort(grp, axis=1), axis=1) > 0).all(axis=1)
+            say(f"  tokens whose four near logits are all distinct: {int(distinct.sum())} of {T}")
     _layers.pop((1, None), None)
     ctx.synth_layer(1, SEED, None)  # restore the synthetic router for later tests
 
