@@ -83,10 +83,9 @@ QE_DEV int xpos(int e) { return (e & 31) * 65 + (e >> 5); } // raw x element e o
 #define L_INV (L_MISC + 16 * 4)                     // f32 [8]          1 / rms of each token
 #define L_SD (L_INV + 8 * 4)                        // f32 [4][8][T]    shared-expert output of the D rows
 #define L_GX (L_SD + 4 * 8 * DEC_T * 4)            // f32 [T][8] the 8 output rows of a group, per token
-#define L_TK (L_GX + DEC_T * 8 * 4)            // top-8 scratch: T = 1: u64 [256] survivor order keys, int [256] their
-                                                    //   experts, u32 [8] logit keys by rank, f32 logit 256;
+#define L_TK (L_GX + DEC_T * 8 * 4)            // top-8 scratch: T = 1: u64 [256] survivor order keys, f32 logit 256;
                                                     //   T > 1: u64 [8][32] survivor keys per token
-#define L_LG (L_TK + 256 * 8 + 256 * 4 + 8 * 4 + 16) // f32 [T][257] the last layer's logits (routing sink)
+#define L_LG (L_TK + 256 * 8 + 16)                   // f32 [T][257] the last layer's logits (routing sink)
 #define L_IORD (L_LG + DEC_T * QE_ROUTER_ROWS * 4)   // int [64] T > 1: items in unit deal order
 #define L_TKF (L_IORD + 64 * 4)                      // u32 [256] T = 1: a survivor's ordered logit by tie key
 #define L_TOTAL (L_TKF + 256 * 4)
@@ -609,10 +608,8 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
             // critical path (they are first needed in D).  (Rounds of wave maxima, or
             // the ranks counted by every thread over all 256, took 1-2 us per layer.)
             uint64_t *s_sk = (uint64_t *)(lds + L_TK);           // [256] survivors' order keys
-            int *s_se = (int *)(lds + L_TK + 2048);                // [256] survivors' experts
-            unsigned *s_rkey = (unsigned *)(lds + L_TK + 3072);    // [8] logit keys by rank
             unsigned *s_full = (unsigned *)(lds + L_TKF);          // [256] survivors' logit keys by tie key
-            float *s_lg256 = (float *)(lds + L_TK + 3104);
+            float *s_lg256 = (float *)(lds + L_TK + 2048);
             if (wv == 0) {
                 uint64_t w[5]; // the lane's four logits and (lane 0) logit 256, one poll loop
                 for (int spins = 0;; ++spins) {
@@ -657,7 +654,6 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
                         const int e = lane + 64 * j, pos = S + (int)__builtin_amdgcn_mbcnt_hi((unsigned)(bal >> 32), __builtin_amdgcn_mbcnt_lo((unsigned)bal, 0u));
                         const unsigned tk = (unsigned)((e & 15) * 16 + (e >> 4));
                         s_sk[pos] = ((uint64_t)v[j] << 32) | (0xffffu - tk);
-                        s_se[pos] = e;
                         s_full[tk] = v[j];
                     }
                     S += (int)__popcll(bal);
@@ -679,14 +675,12 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
                         if (lane < QE_K_USED) {
                             const unsigned tk = 0xffu - (k32 & 0xffu); // (e % 16) * 16 + e / 16
                             s_items[lane] = make_int4((int)(((tk & 15u) << 4) | ((tk >> 4) & 15u)), lane, 1, 0);
-                            s_rkey[lane] = s_full[tk];
                         }
                     } else {
                         sort32_desc_u64(khi, klo, lane);
                         if (lane < QE_K_USED) {
                             const unsigned tk = 0xffffu - (klo & 0xffffu);
                             s_items[lane] = make_int4((int)(((tk & 15u) << 4) | ((tk >> 4) & 15u)), lane, 1, 0);
-                            s_rkey[lane] = khi;
                         }
                     }
                 } else {
@@ -700,8 +694,8 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
                         }
                         for (; j < S; ++j) r += (int)(s_sk[j] > ki);
                         if (i < S && r < QE_K_USED) {
-                            s_items[r] = make_int4(s_se[i] & (QE_N_EXPERT - 1), r, 1, 0);
-                            s_rkey[r] = (unsigned)(ki >> 32);
+                            const unsigned tk = 0xffffu - ((unsigned)ki & 0xffffu);
+                            s_items[r] = make_int4((int)(((tk & 15u) << 4) | ((tk >> 4) & 15u)), r, 1, 0);
                         }
                     }
                 }
@@ -943,10 +937,12 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
         if (TM == 1 && wv == NWV - 1) {
             // weights and shared gate of the selection (read after the h wait), by a
             // wave the shared down rows leave idle
-            const unsigned *s_rkey = (const unsigned *)(lds + L_TK + 3072);
-            const int myid = lane < QE_K_USED ? s_items[lane].x & (QE_N_EXPERT - 1) : 0;
-            const float mine = ord2f(s_rkey[lane < QE_K_USED ? lane : 0]), sel0 = ord2f(s_rkey[0]);
-            topk_finish(mine, myid, sel0, *(const float *)(lds + L_TK + 3104), lane, s_ids, s_wts, s_shg);
+            // the selected experts' logit keys, written by the survivors in G (by tie key)
+            const unsigned *s_full = (const unsigned *)(lds + L_TKF);
+            auto tkey = [](int e) { return (e & 15) * 16 + (e >> 4); };
+            const int myid = lane < QE_K_USED ? s_items[lane].x & (QE_N_EXPERT - 1) : s_items[0].x & (QE_N_EXPERT - 1);
+            const float mine = ord2f(s_full[tkey(myid)]), sel0 = ord2f(s_full[tkey(s_items[0].x & (QE_N_EXPERT - 1))]);
+            topk_finish(mine, myid, sel0, *(const float *)(lds + L_TK + 2048), lane, s_ids, s_wts, s_shg);
         }
         // The shared down rows of every D row group run first, while the routed
         // h is still on its way: wave (rr, half 0), 16-lane group g takes tokens
