@@ -474,23 +474,6 @@ QE_HD size_t qe_hl_off(int K, int row, int k) {
 QE_DEV uint32_t pack_h2(_Float16 a, _Float16 b) {
     return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
 }
-// Split the 32 values of block b of row `row` and store them in that layout.
-QE_DEV void store_hilo_block(const float v[32], uint8_t *base, int K, int row, int b) {
-#pragma unroll
-    for (int g = 0; g < 4; ++g) { // 8 consecutive elements 8g..8g+7
-        uint32_t h[4], l[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float x0 = v[8 * g + 2 * i], x1 = v[8 * g + 2 * i + 1];
-            const _Float16 a0 = (_Float16)x0, a1 = (_Float16)x1;
-            h[i] = pack_h2(a0, a1);
-            l[i] = pack_h2((_Float16)(x0 - (float)a0), (_Float16)(x1 - (float)a1));
-        }
-        uint8_t *dst = base + qe_hl_off(K, row, 32 * b + 8 * g);
-        *(uint4 *)dst = make_uint4(h[0], h[1], h[2], h[3]);
-        *(uint4 *)(dst + QE_HL_LO) = make_uint4(l[0], l[1], l[2], l[3]);
-    }
-}
 
 QE_DEV void load32(const float *p, float v[32]) {
     const float4 *q = (const float4 *)p;

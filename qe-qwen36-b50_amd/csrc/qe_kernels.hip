@@ -18,46 +18,84 @@
 // ===========================================================================
 // wave per token: xn, xq, xs, and router row 256 (the shared-expert gate) as a
 // canonical wave dot while the token's xn sits in registers (lane l holds
-// elements [32l, 32l+32)), so k_topk need not read xn again
-__global__ __launch_bounds__(256) void k_normq(const float *x, int T, const float *post_norm, float *xn, int8_t *xqp,
-                                               float *xs, _Float16 *xhl, int32_t *chunk_hist, int nch, const float *W,
-                                               float *logits) {
-    // the workgroup's four rows move through LDS: coalesced float4 loads and
-    // stores of the rows, lane c of wave w working on elements [32c, 32c+32) of
-    // row w (chunks padded to 33 words: conflict-free both ways)
-    __shared__ float s_r[4][64 * 33];
-    // the 8 workgroups of a 32-token tile of xhl run on one XCD (b % 8), so the
-    // tile's lines are completed in one L2: b = 64 G + 8 s + x -> tokens
-    // 32 (8 G + x) + 4 s .. + 3
+// elements [32l, 32l+32)), so k_topk need not read xn again.  Workgroup of
+// NQ_TOK tokens (one wave each): 8 from QE_NQ8_T tokens on, 4 below (twice the
+// workgroups where there are few).
+#define NQ_RSTR (64 * 33 + 1) /* LDS row stride (floats): the rows' same element in different banks */
+#ifndef QE_NQ8_T
+#define QE_NQ8_T 2048
+#endif
+template <int NQ_TOK>
+__global__ __launch_bounds__(64 * NQ_TOK) void k_normq(const float *x, int T, const float *post_norm, float *xn, int8_t *xqp,
+                                                      float *xs, _Float16 *xhl, int32_t *chunk_hist, int nch, const float *W,
+                                                      float *logits) {
+    constexpr int WPT = 32 / NQ_TOK; // workgroups per 32-token tile
+    // the workgroup's rows move through LDS: coalesced float4 loads and stores of
+    // the rows, lane c of wave w working on elements [32c, 32c+32) of row w
+    // (chunks padded to 33 words: conflict-free both ways)
+    __shared__ float s_r[NQ_TOK * NQ_RSTR];
+    // the WPT workgroups of a 32-token tile of xhl run on one XCD (b % 8):
+    // b = 8 WPT G + 8 s + x -> tokens 32 (8 G + x) + NQ_TOK s .. + NQ_TOK - 1
     const int b = blockIdx.x;
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, t0 = 32 * (8 * (b >> 6) + (b & 7)) + 4 * ((b >> 3) & 7),
-              t = t0 + wv;
-    if ((int)blockIdx.x < nch) chunk_hist[blockIdx.x * QE_N_EXPERT + tid] = 0; // dispatch histogram
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6,
+              t0 = 32 * (8 * (b / (8 * WPT)) + (b & 7)) + NQ_TOK * ((b >> 3) % WPT), t = t0 + wv;
+    if (b < nch && tid < QE_N_EXPERT) chunk_hist[b * QE_N_EXPERT + tid] = 0; // dispatch histogram
+    constexpr int F4 = QE_D / 4 / (64 * NQ_TOK); // float4s of a row per thread
 #pragma unroll
-    for (int i = 0; i < 8; ++i) { // row i / 2, float4 (i & 1) * 256 + tid
-        const int r = i >> 1, f = (i & 1) * 256 + tid, e = 4 * f;
-        if (t0 + r < T) {
-            const float4 q = ((const float4 *)(x + (size_t)(t0 + r) * QE_D))[f];
-            float *s = &s_r[r][(e >> 5) * 33 + (e & 31)];
-            s[0] = q.x; s[1] = q.y; s[2] = q.z; s[3] = q.w;
+    for (int r = 0; r < NQ_TOK; ++r) // row r, float4s tid + 64 NQ_TOK h
+#pragma unroll
+        for (int h = 0; h < F4; ++h) {
+            const int f = tid + 64 * NQ_TOK * h, e = 4 * f;
+            if (t0 + r < T) {
+                const float4 q = ((const float4 *)(x + (size_t)(t0 + r) * QE_D))[f];
+                float *sp = &s_r[r * NQ_RSTR + (e >> 5) * 33 + (e & 31)];
+                sp[0] = q.x; sp[1] = q.y; sp[2] = q.z; sp[3] = q.w;
+            }
         }
-    }
     __syncthreads();
     float v[32];
     if (t < T) {
 #pragma unroll
-        for (int i = 0; i < 32; ++i) v[i] = s_r[wv][lane * 33 + i];
+        for (int i = 0; i < 32; ++i) v[i] = s_r[wv * NQ_RSTR + lane * 33 + i];
         wave_norm_chunk(v, post_norm, lane);
 #pragma unroll
-        for (int i = 0; i < 32; ++i) s_r[wv][lane * 33 + i] = v[i];
+        for (int i = 0; i < 32; ++i) s_r[wv * NQ_RSTR + lane * 33 + i] = v[i];
     }
     __syncthreads();
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int r = i >> 1, f = (i & 1) * 256 + tid, e = 4 * f;
-        if (t0 + r < T) {
-            const float *s = &s_r[r][(e >> 5) * 33 + (e & 31)];
-            ((float4 *)(xn + (size_t)(t0 + r) * QE_D))[f] = make_float4(s[0], s[1], s[2], s[3]);
+    for (int r = 0; r < NQ_TOK; ++r)
+#pragma unroll
+        for (int h = 0; h < F4; ++h) {
+            const int f = tid + 64 * NQ_TOK * h, e = 4 * f;
+            if (t0 + r < T) {
+                const float *sp = &s_r[r * NQ_RSTR + (e >> 5) * 33 + (e & 31)];
+                ((float4 *)(xn + (size_t)(t0 + r) * QE_D))[f] = make_float4(sp[0], sp[1], sp[2], sp[3]);
+            }
+        }
+    {   // xn as fp16 hi/lo halves in the tile order of the shared-expert MFMA tiles
+        // (qe_hl_off): thread (token i = tid % NQ_TOK, q = tid / NQ_TOK) takes groups
+        // j = q + 64 k (block j / 4, 8 elements 8 (j % 4) ..); the tokens' pieces of one
+        // group are consecutive 16-byte slots of a chunk, so the NQ_TOK lanes of a group
+        // store one aligned run of 16 NQ_TOK bytes (a whole 128-byte line at 8 tokens)
+        // instead of NQ_TOK separate pieces
+        const int i = tid & (NQ_TOK - 1), q = tid / NQ_TOK;
+        if (t0 + i < T) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int j = q + 64 * k, bb = j >> 2, g = j & 3;
+                const float *sp = &s_r[i * NQ_RSTR + bb * 33 + 8 * g];
+                uint32_t hw[4], lw[4];
+#pragma unroll
+                for (int m = 0; m < 4; ++m) {
+                    const float x0 = sp[2 * m], x1 = sp[2 * m + 1];
+                    const _Float16 a0 = (_Float16)x0, a1 = (_Float16)x1;
+                    hw[m] = pack_h2(a0, a1);
+                    lw[m] = pack_h2((_Float16)(x0 - (float)a0), (_Float16)(x1 - (float)a1));
+                }
+                uint8_t *dst = (uint8_t *)xhl + qe_hl_off(QE_D, t0 + i, 32 * bb + 8 * g);
+                *(uint4 *)dst = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+                *(uint4 *)(dst + QE_HL_LO) = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+            }
         }
     }
     if (t >= T) return;
@@ -75,7 +113,6 @@ __global__ __launch_bounds__(256) void k_normq(const float *x, int T, const floa
         const float lg = wave_sum_canon(acc);
         if (lane == 0) logits[(size_t)t * QE_ROUTER_ROWS + QE_N_EXPERT] = lg;
     }
-    store_hilo_block(v, (uint8_t *)xhl, QE_D, t, lane);
     lane_quant_store_opnd(v, xqp + (size_t)t * QE_D, lane, xs + (size_t)t * (QE_D / 32) + lane);
 }
 
@@ -337,8 +374,13 @@ hipError_t qe_launch_layer(const QeLayerPtrs &L, const QeScratch &S, const float
     QeCombineArgs da{T, S.yp, S.sd, S.shg, x2, out, exit_norm, exit_xn};
     {
         QE_PROF(QP_NORMQ);
-        k_normq<<<64 * ((T + 255) / 256), 256, 0, st>>>(xin, T, pn, S.xn, S.xqp, S.xs, S.xhl, S.chunk_hist,
-                                              (T * QE_K_USED + 1023) / 1024, L.router, S.logits);
+        const int nch = (T * QE_K_USED + 1023) / 1024;
+        if (T >= QE_NQ8_T)
+            k_normq<8><<<32 * ((T + 255) / 256), 512, 0, st>>>(xin, T, pn, S.xn, S.xqp, S.xs, S.xhl, S.chunk_hist, nch,
+                                                                 L.router, S.logits);
+        else
+            k_normq<4><<<64 * ((T + 255) / 256), 256, 0, st>>>(xin, T, pn, S.xn, S.xqp, S.xs, S.xhl, S.chunk_hist, nch,
+                                                                 L.router, S.logits);
     }
     {
         QE_PROF(QP_ROUTER);
