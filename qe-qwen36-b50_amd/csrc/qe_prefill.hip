@@ -380,18 +380,31 @@ __device__ __forceinline__ void expert_tile(const GemmTileArgs &a, const int4 it
                 if (n == 0) amax[wv][16 * t + 4 * g + i] = m[t][i];
             }
         __syncthreads();
+        // The workgroup's h of a pair is the 64 contiguous bytes [64 yb, 64 yb + 64) of its
+        // row in the operand layout (blocks 2 yb, 2 yb + 1), and its two block scales are
+        // adjacent: both are assembled in LDS (after the maxima, in the same free stage)
+        // and stored 16 bytes per thread, instead of one byte per lane and value.
+        uint8_t *htile = sm.raw + LY::ACT + (NCH & 1) * LY::ACT_SZ + 4 * QE_MFMA_MC * 4; // [16 NT][64]
+        float *stile = (float *)(htile + 16 * NT * 64);                                  // [16 NT][2]
+        static_assert(4 * QE_MFMA_MC * 4 + 16 * NT * (64 + 8) <= LY::ACT_SZ, "h tile fits the free stage");
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
+                const int mi = 16 * t + 4 * g + i;
                 float d;
-                const float id = quant_scale_inv(fmaxf(m[t][i], amax[wv ^ 1][16 * t + 4 * g + i]), d);
-                const int p = s_pair[16 * t + 4 * g + i];
-                if (p >= 0) {
-                    int8_t *hrow = a.hq + (size_t)p * QE_FF_EXP + (jb >> 1) * 64 + (n >> 2) * 16 + (jb & 1) * 8 + (n & 3);
-                    hrow[4 * half] = quant_one(h[t][i], id);
-                    if (n == 0 && half == 0) a.hs[(size_t)p * (QE_FF_EXP / 32) + jb] = d;
-                }
+                const float id = quant_scale_inv(fmaxf(m[t][i], amax[wv ^ 1][mi]), d);
+                htile[mi * 64 + (n >> 2) * 16 + (jb & 1) * 8 + (n & 3) + 4 * half] = (uint8_t)quant_one(h[t][i], id);
+                if (n == 0 && half == 0) stile[mi * 2 + (jb & 1)] = d;
+            }
+        }
+        __syncthreads();
+        {   // thread (pair tid / 4, 16-byte part tid % 4)
+            const int mi = tid >> 2, q = tid & 3;
+            const int p = mi < 16 * NT ? s_pair[mi] : -1;
+            if (p >= 0) {
+                *(uint4 *)(a.hq + (size_t)p * QE_FF_EXP + (jb >> 1) * 64 + 16 * q) = *(const uint4 *)(htile + mi * 64 + 16 * q);
+                if (q == 0) *(float2 *)(a.hs + (size_t)p * (QE_FF_EXP / 32) + 2 * (jb >> 1)) = *(const float2 *)(stile + mi * 2);
             }
         }
     } else {
@@ -1042,17 +1055,23 @@ __device__ __forceinline__ void dn_tile(const GemmTileArgs &a, const int4 it, co
                     asm volatile("" : "+v"(acc[c][t][0]), "+v"(acc[c][t][1]), "+v"(acc[c][t][2]), "+v"(acc[c][t][3]));
         }
         if (Q == 3) { // the row group is complete: yp[p][row] = w_p * y, accumulators cleared
+            // lane n holds rows n (c = 0) and 16 + n (c = 1) of the wave's 32; lanes n and
+            // n ^ 1 swap a value, so the even one stores rows n, n + 1 and the odd one rows
+            // 15 + n, 16 + n as 8-byte pairs: the 16 lanes of a pair write its 128 bytes
+            // as one line instead of two half lines
             const int rg = rg0 + (qi >> 2);
+            const bool odd = n & 1;
 #pragma unroll
             for (int t = 0; t < NT; ++t)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const int m = 16 * t + 4 * g + i, pm = sm.pair[m];
+                    const float w = sm.w[m];
+                    const float y0 = w * acc[0][t][i], y1 = w * acc[1][t][i];
+                    const float p0 = dpp_f<QE_DPP_XOR1>(y0), p1 = dpp_f<QE_DPP_XOR1>(y1);
                     if (pm >= 0) {
-                        const float w = sm.w[m];
-                        float *yrow = a.yp + (size_t)pm * QE_D + 128 * rg + 32 * wv + n;
-#pragma unroll
-                        for (int c = 0; c < NC; ++c) yrow[16 * c] = w * acc[c][t][i];
+                        float *yrow = a.yp + (size_t)pm * QE_D + 128 * rg + 32 * wv;
+                        *(float2 *)(yrow + (odd ? 15 + n : n)) = odd ? make_float2(p1, y1) : make_float2(y0, p0);
                     }
 #pragma unroll
                     for (int c = 0; c < NC; ++c) acc[c][t][i] = 0.f;
