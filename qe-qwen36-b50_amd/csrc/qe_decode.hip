@@ -837,9 +837,12 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
         auto no_prefetch = []() {};
         if constexpr (TM == 1) {
             // The shared-expert activations (written in R) are read here, their
-            // loads in flight with the unit's, instead of on the h wait in D.
+            // loads in flight with the unit's, instead of on the h wait in D; they
+            // are issued behind the unit's rows, which every workgroup requests at
+            // once and whose drain from HBM bounds this stage (issued first, they
+            // had cost 1.6 %).
             uint64_t hsh_w = 0;
-            if (tid < QE_FF_SH) hsh_w = LD_A((uint64_t *)EXr + EX_HSH + tid);
+            bool hsh_issued = false;
             for (int unit = blockIdx.x; unit < nunits; unit += gridDim.x) {
                 const int4 it = s_items[unit / upi];
                 const int j = (unit % upi) * JU + wv, c = lane & 31;
@@ -851,6 +854,7 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
                 const uint4 xa = *(const uint4 *)(s_xq + c * 32), xb = *(const uint4 *)(s_xq + c * 32 + 16);
                 const uint4 xc = *(const uint4 *)(s_xq + (c + 32) * 32), xd = *(const uint4 *)(s_xq + (c + 32) * 32 + 16);
                 const float xs0 = s_xs[c], xs1 = s_xs[c + 32];
+                if (!hsh_issued) { hsh_issued = true; if (tid < QE_FF_SH) hsh_w = LD_A((uint64_t *)EXr + EX_HSH + tid); }
                 __builtin_amdgcn_sched_barrier(0);
                 const float d0 = f16_bits_to_f32(r0) * xs0, d1 = f16_bits_to_f32(r1) * xs1;
                 float acc = d0 * (float)nl4_block_dot(nl4_decode_block<true>(q0), xa, xb);
@@ -871,7 +875,7 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
                 if (lane < REP) ST_A(EX + lane * EX_TOTAL + EX_HF + (size_t)p * QE_FF_EXP + j, pack_tv(h, tagG));
             }
             if ((int)blockIdx.x >= nunits && tid < QE_FF_SH) { // no unit here
-                uint64_t w1[1] = {hsh_w};
+                uint64_t w1[1] = {LD_A((uint64_t *)EXr + EX_HSH + tid)};
                 if ((unsigned)(w1[0] >> 32) != tagR) read_tv<1>(EXr + EX_HSH + tid, 0, tagR, w1, true, pc);
                 s_hsh[tid] = tv_val(w1[0]);
             }
