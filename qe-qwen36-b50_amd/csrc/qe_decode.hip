@@ -600,10 +600,11 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
             // lane's maximum over its four, then over groups of 8 lanes, gives eight
             // maxima of distinct experts; the smallest of them bounds the 8th largest
             // logit from below, so the experts at or above it (about 18 of 256) hold
-            // the top 8.  Each of these survivors counts the survivors ahead of it in
-            // the reference's total order (larger value first, ties to the smaller
-            // (e % 16, e / 16)), one 64-bit comparison of {ordered value, 0xffff -
-            // tie key} each: ranks 0..7 are the selection in order.  The experts
+            // the top 8.  The survivors are put in the reference's total order (larger
+            // value first, ties to the smaller (e % 16, e / 16)) by their keys {ordered
+            // value, 0xffff - tie key}: up to 32 of them sorted in registers, more (many
+            // equal logits) ranked by counting the keys above each; ranks 0..7 are the
+            // selection in order.  The experts
             // become the items in rank order; the weights are formed later, off the
             // critical path (they are first needed in D).  (Rounds of wave maxima, or
             // the ranks counted by every thread over all 256, took 1-2 us per layer.)
