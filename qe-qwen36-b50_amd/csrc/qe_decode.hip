@@ -84,8 +84,8 @@ QE_DEV int xpos(int e) { return (e & 31) * 65 + (e >> 5); } // raw x element e o
 #define L_SD (L_INV + 8 * 4)                        // f32 [4][8][T]    shared-expert output of the D rows
 #define L_GX (L_SD + 4 * 8 * DEC_T * 4)            // f32 [T][8] the 8 output rows of a group, per token
 #define L_TK (L_GX + DEC_T * 8 * 4)            // top-8 scratch: T = 1: u64 [256] survivor order keys, f32 logit 256;
-                                                    //   T > 1: u64 [8][32] survivor keys per token
-#define L_LG (L_TK + 256 * 8 + 16)                   // f32 [T][257] the last layer's logits (routing sink)
+                                                    //   T > 1: u64 [8][64] survivor keys per token
+#define L_LG (L_TK + 512 * 8 + 16)                   // f32 [T][257] the last layer's logits (routing sink)
 #define L_IORD (L_LG + DEC_T * QE_ROUTER_ROWS * 4)   // int [64] T > 1: items in unit deal order
 #define L_TKF (L_IORD + 64 * 4)                      // u32 [256] T = 1: a survivor's ordered logit by tie key
 #define L_TOTAL (L_TKF + 256 * 4)
@@ -602,7 +602,7 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
             // logit from below, so the experts at or above it (about 18 of 256) hold
             // the top 8.  The survivors are put in the reference's total order (larger
             // value first, ties to the smaller (e % 16, e / 16)) by their keys {ordered
-            // value, 0xffff - tie key}: up to 32 of them sorted in registers, more (many
+            // value, 0xffff - tie key}: up to 64 of them sorted in registers, more (many
             // equal logits) ranked by counting the keys above each; ranks 0..7 are the
             // selection in order.  The experts
             // become the items in rank order; the weights are formed later, off the
@@ -659,9 +659,10 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
                     }
                     S += (int)__popcll(bal);
                 }
-                if (S <= 32) {
-                    // up to 32 survivors: one per lane, sorted in registers (no LDS round
-                    // trips); a key's low half holds 0xffff - tie key, so it names its expert
+                if (S <= 64) {
+                    // up to 64 survivors: one per lane, sorted in registers (no LDS round
+                    // trips; the 64-wide stage only when more than 32 survive); a key's low
+                    // half holds 0xffff - tie key, so it names its expert
                     const uint64_t ki = lane < S ? s_sk[lane] : 0ull; // real keys are never 0
                     uint32_t khi = (uint32_t)(ki >> 32), klo = (uint32_t)ki;
                     // First on 32-bit keys {top 24 bits of the ordered value, 0xff - tie key}:
@@ -671,6 +672,7 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
                     // logit is >= 2^23, so real keys stay above the padding's 0.)
                     uint32_t k32 = (khi & 0xffffff00u) | (klo & 0xffu);
                     sort32_desc_u32(k32, lane);
+                    if (S > 32) merge64_desc_u32(k32, lane);
                     const uint32_t nx = dpp_u<0x101>(k32); // row_shl:1, the next rank
                     if (!__any(lane < QE_K_USED && ((k32 ^ nx) >> 8) == 0u)) {
                         if (lane < QE_K_USED) {
@@ -679,6 +681,7 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
                         }
                     } else {
                         sort32_desc_u64(khi, klo, lane);
+                        if (S > 32) merge64_desc_u64(khi, klo, lane);
                         if (lane < QE_K_USED) {
                             const unsigned tk = 0xffffu - (klo & 0xffffu);
                             s_items[lane] = make_int4((int)(((tk & 15u) << 4) | ((tk >> 4) & 15u)), lane, 1, 0);
@@ -730,7 +733,7 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
                 for (int j = 0; j < 4; ++j) s_lgs[lane + 64 * j] = v[j];
                 if (lane == 0) s_lgs[QE_N_EXPERT] = v[4];
             }
-            wave_topk_sorted(v, v[4], lane, (uint64_t *)(lds + L_TK) + 32 * t, s_ids + t * QE_K_USED, s_wts + t * QE_K_USED,
+            wave_topk_sorted(v, v[4], lane, (uint64_t *)(lds + L_TK) + 64 * t, s_ids + t * QE_K_USED, s_wts + t * QE_K_USED,
                              s_shg + t);
         }
         __syncthreads();

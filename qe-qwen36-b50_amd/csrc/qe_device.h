@@ -236,6 +236,43 @@ QE_DEV void sort32_desc_u32(uint32_t &k, int lane) {
     xor1();
 }
 
+// Lane 63 - i's value (the mirror across the wave): the row mirror of lane
+// i ^ 32, then of lane i ^ 48.  And lane i ^ 16's value.
+QE_DEV uint32_t lane_mirror64(uint32_t v, int lane) {
+    unsigned a, b, c, d;
+    rows32(dpp_u<QE_DPP_MIRROR>(v), a, b);
+    rows16((lane & 32) ? a : b, c, d);
+    return (lane & 16) ? c : d;
+}
+QE_DEV uint32_t lane_xor16(uint32_t v, int lane) {
+    unsigned a, b;
+    rows16(v, a, b);
+    return (lane & 16) ? a : b;
+}
+// The last stage (k = 64) of the bitonic network: with lanes 0..31 and 32..63
+// each sorted descending (sort32_desc_*), the wave becomes one descending run.
+QE_DEV void merge64_desc_u32(uint32_t &k, int lane) {
+    cx32(k, lane_mirror64(k, lane), !(lane & 32));
+    cx32(k, lane_xor16(k, lane), !(lane & 16));
+    cx32(k, dpp_u<0x128>(k), !(lane & 8)); // row_ror:8 = xor 8
+    const bool up = lane & 4;
+    const uint32_t r = dpp_u<0x114>(k), l = dpp_u<0x104>(k);
+    cx32(k, up ? r : l, !up);
+    cx32(k, dpp_u<QE_DPP_XOR2>(k), !(lane & 2));
+    cx32(k, dpp_u<QE_DPP_XOR1>(k), !(lane & 1));
+}
+QE_DEV void merge64_desc_u64(uint32_t &hi, uint32_t &lo, int lane) {
+    cx64(hi, lo, lane_mirror64(hi, lane), lane_mirror64(lo, lane), !(lane & 32));
+    cx64(hi, lo, lane_xor16(hi, lane), lane_xor16(lo, lane), !(lane & 16));
+    cx64(hi, lo, dpp_u<0x128>(hi), dpp_u<0x128>(lo), !(lane & 8));
+    const bool up = lane & 4;
+    const uint32_t rh = dpp_u<0x114>(hi), lh = dpp_u<0x104>(hi);
+    const uint32_t rl = dpp_u<0x114>(lo), ll = dpp_u<0x104>(lo);
+    cx64(hi, lo, up ? rh : lh, up ? rl : ll, !up);
+    cx64(hi, lo, dpp_u<QE_DPP_XOR2>(hi), dpp_u<QE_DPP_XOR2>(lo), !(lane & 2));
+    cx64(hi, lo, dpp_u<QE_DPP_XOR1>(hi), dpp_u<QE_DPP_XOR1>(lo), !(lane & 1));
+}
+
 QE_DEV unsigned wave_min_u32(unsigned v) {
     v = umin32(v, dpp_ub<QE_DPP_XOR1>(v));
     v = umin32(v, dpp_ub<QE_DPP_XOR2>(v));
@@ -332,13 +369,15 @@ QE_DEV int wave_topk_vals(const float v_in[4], float lg_sh, int lane, int32_t *i
 // The same selection, usually in fewer steps: each lane's maximum over its
 // four, then over groups of 8 lanes, gives eight maxima of distinct experts;
 // the smallest of them bounds the 8th largest logit from below, so the experts
-// at or above it (about 18 of 256) hold the top 8.  Up to 32 of them go one per
-// lane through `sk` (32 words of LDS) as 64-bit keys {ordered value, 0xffff -
-// tie key} and are sorted in registers; lanes 0..7 then hold the selection in
-// the reference's order.  More survivors (many equal logits) take the rounds
-// of wave_topk_vals.
-QE_DEV void wave_topk_sorted(const float v_in[4], float lg_sh, int lane, uint64_t *sk, int32_t *ids, float *wts,
-                             float *shg) {
+// at or above it (about 20 of 256; more than 32 for 7 % of random tokens, more
+// than 64 for 0.05 %) hold the top 8.  Up to 64 of them go one per lane through `sk` (64 words of
+// LDS) as 64-bit keys {ordered value, 0xffff - tie key} and are sorted in
+// registers (the 64-wide stage only when more than 32 survive); lanes 0..7
+// then hold the selection in the reference's order.  More survivors (many
+// equal logits) take the rounds of wave_topk_vals.  Returns, in lane k < 8,
+// the k-th selected expert.
+QE_DEV int wave_topk_sorted(const float v_in[4], float lg_sh, int lane, uint64_t *sk, int32_t *ids, float *wts,
+                            float *shg) {
     unsigned v[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) v[j] = f2ord(v_in[j] + 0.0f);
@@ -359,20 +398,19 @@ QE_DEV void wave_topk_sorted(const float v_in[4], float lg_sh, int lane, uint64_
         const unsigned long long bal = __ballot(sv);
         const int pos = S + (int)__builtin_amdgcn_mbcnt_hi((unsigned)(bal >> 32), __builtin_amdgcn_mbcnt_lo((unsigned)bal, 0u));
         const int e = lane + 64 * j;
-        if (sv && pos < 32) sk[pos] = ((uint64_t)v[j] << 32) | (0xffffu - (unsigned)((e & 15) * 16 + (e >> 4)));
+        if (sv && pos < 64) sk[pos] = ((uint64_t)v[j] << 32) | (0xffffu - (unsigned)((e & 15) * 16 + (e >> 4)));
         S += (int)__popcll(bal);
     }
-    if (S > 32) {
-        wave_topk_vals(v_in, lg_sh, lane, ids, wts, shg);
-        return;
-    }
+    if (S > 64) return wave_topk_vals(v_in, lg_sh, lane, ids, wts, shg);
     const uint64_t ki = lane < S ? sk[lane] : 0ull; // real keys are never 0
     uint32_t khi = (uint32_t)(ki >> 32), klo = (uint32_t)ki;
     sort32_desc_u64(khi, klo, lane);
+    if (S > 32) merge64_desc_u64(khi, klo, lane);
     const unsigned tk = 0xffffu - (klo & 0xffffu); // (e % 16) * 16 + e / 16
     const int myid = (int)(((tk & 15u) << 4) | ((tk >> 4) & 15u));
     const float sel0 = ord2f((unsigned)__builtin_amdgcn_readfirstlane(khi));
     topk_finish(ord2f(khi), myid, sel0, lg_sh, lane, ids, wts, shg);
+    return myid;
 }
 // Canonical RMSNorm sum of squares of a 2048-vector: 256 groups of 8
 // contiguous elements, each an fma chain from 0 in index order, combined by the

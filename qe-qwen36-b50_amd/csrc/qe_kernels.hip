@@ -119,13 +119,15 @@ __global__ __launch_bounds__(64 * NQ_TOK) void k_normq(const float *x, int T, co
 static_assert(RT_SPLIT == 8, "k_topk merges eight router partials");
 
 // Wave per token, 4 tokens per workgroup: logits (router partials merged +
-// bias; row 256 came from k_normq), then top-8, weights and the shared gate
+// bias; row 256 came from k_normq), then top-8 (the survivors of a group-maximum
+// threshold sorted in registers), weights and the shared gate
 // (engine/qe.cpp:1454-1483).  The workgroup then adds its 32 expert ids
 // to the dispatch histogram of its 1024-pair chunk (zeroed by k_normq), one
 // global add per distinct expert.
 __global__ __launch_bounds__(256) void k_topk(const float *part, const float *bias, int T, float *logits, int32_t *ids,
                                               float *wts, float *shg, int32_t *chunk_hist) {
     __shared__ int s_h[QE_N_EXPERT];
+    __shared__ uint64_t s_sk[4][64]; // each wave's survivor keys
     const int lane = threadIdx.x & 63, t = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (threadIdx.x < QE_N_EXPERT) s_h[threadIdx.x] = 0;
     __syncthreads();
@@ -145,7 +147,7 @@ __global__ __launch_bounds__(256) void k_topk(const float *part, const float *bi
         logits[(size_t)t * QE_ROUTER_ROWS + e] = x;
     }
     const float lg = logits[(size_t)t * QE_ROUTER_ROWS + QE_N_EXPERT];
-    const int e = wave_topk_vals(v, lg, lane, ids + t * QE_K_USED, wts + t * QE_K_USED, shg + t);
+    const int e = wave_topk_sorted(v, lg, lane, s_sk[threadIdx.x >> 6], ids + t * QE_K_USED, wts + t * QE_K_USED, shg + t);
     if (lane < QE_K_USED) atomicAdd(&s_h[e], 1);
     }
     __syncthreads();

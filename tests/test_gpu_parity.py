@@ -317,6 +317,70 @@ def test_topk_ties_on_gpu(ctx, torch_cuda, kind, T):
     ctx.synth_layer(1, SEED, None)  # restore the synthetic router for later tests
 
 
+def survivor_count(lg):
+    """Experts at or above the smallest of the eight group maxima (a group is
+    the 32 experts l + 64 j of lanes l = 8 g .. 8 g + 7), per token: the
+    candidates the GPU top-8 sorts."""
+    v = lg[:, :256]
+    g = v.reshape(-1, 4, 8, 8).max(axis=(1, 3)).min(axis=1)
+    return (v >= g[:, None]).sum(axis=1)
+
+
+def survivor_bias(S, seed):
+    """A router bias (steps of 25, far above the dot's few units) that orders
+    the experts so that exactly S survive: group 0's largest expert is the
+    S-th largest, and every other group has one among the S - 1 above it."""
+    rng = np.random.default_rng(seed)
+    e = np.arange(256)
+    grp = (e & 63) >> 3
+    firsts = [int(rng.choice(e[grp == g])) for g in range(1, 8)]
+    others = [int(i) for i in rng.permutation(e[grp != 0]) if i not in firsts]
+    g0 = [int(i) for i in rng.permutation(e[grp == 0])]
+    top = firsts + others[:S - 8]
+    rng.shuffle(top)
+    order = top + g0[:1] + others[S - 8:] + g0[1:]
+    bias = np.empty(256, np.float32)
+    bias[order] = 25.0 * (255 - np.arange(256, dtype=np.float32))
+    return bias, order
+
+
+@pytest.mark.parametrize("S,tie", [(33, False), (33, True), (64, False), (64, True), (65, False), (100, False)])
+@pytest.mark.parametrize("T", [1, 5, 64])
+def test_topk_survivor_counts(ctx, torch_cuda, S, tie, T):
+    # 33..64 survivors take the 64-wide register sort (T = 1 decode, T > 1
+    # decode, and the prefill top-8), more take the fallbacks (ranks counted in
+    # LDS at T = 1, rounds of wave maxima otherwise).  "tie": the experts ranked
+    # 3rd and 4th get one router row and one bias, so their logits are equal and
+    # T = 1 takes its 64-bit sort
+    say(f"top-8 with {S} survivors{' and a tie' if tie else ''}, T={T}")
+    bias, order = survivor_bias(S, 900 + S)
+    L = O.SynthLayer(SEED, 1, bias=bias)
+    if tie:
+        a, b = order[2], order[3]
+        bias[b] = bias[a]
+        L.bias = bias
+        R = L.router.copy()
+        R[b] = R[a]
+        L.router = np.ascontiguousarray(R, np.float32)
+    x = O.gen_x(SEED, 700 + T, T)
+    lg = O.router(x, L.router, L.bias)
+    assert (survivor_count(lg) == S).all()
+    if tie:
+        assert (lg[:, order[2]] == lg[:, order[3]]).all()
+    ctx.synth_layer(1, SEED, bias)
+    if tie:
+        ctx.set_dense(1, router=L.router)
+    xd = torch_cuda.from_numpy(x).cuda()
+    y = torch_cuda.empty_like(xd)
+    ctx.forward_normed(1, xd, y, T)
+    torch_cuda.cuda.synchronize()
+    g = ctx.routing(T)
+    g["logits"] = ctx.logits(T)
+    g["out"] = y.cpu().numpy()
+    check_layer(L, g, x)
+    ctx.synth_layer(1, SEED, None)  # restore the synthetic router for later tests
+
+
 class PackLayer:
     """Oracle view of a layer loaded from a pack (same bytes the loader uploads)."""
 
