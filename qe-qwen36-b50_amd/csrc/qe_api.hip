@@ -160,7 +160,7 @@ int qe_moe_create(int device, int n_layers, int t_max, qe_moe_ctx **out) {
     A(S.off, (QE_N_EXPERT + 1) * 4);
     A(S.pairs, NP * 4);
     A(S.items, max_items * sizeof(int4));
-    A(S.n_items, 4);
+    A(S.n_items, 8);
     A(S.hqp, NP * QE_FF_EXP);
     A(S.hs, NP * (QE_FF_EXP / 32) * 4);
     A(S.sd, T * QE_D * 4);

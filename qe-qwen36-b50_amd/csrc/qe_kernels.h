@@ -57,7 +57,7 @@ struct QeScratch {
     float *rpart;                           // [8][T][256] router subtree partials
     int32_t *ids; float *wts; float *shg;   // [T][8], [T][8], [T]
     int32_t *off; int32_t *pairs;           // [257], [T*8]
-    int4 *items; int32_t *n_items;          // work items (expert, first pair, count)
+    int4 *items; int32_t *n_items;          // work items (expert, first pair, count); n_items[0] items, the first n_items[1] big
     int8_t *hqp; float *hs;                 // [T*8][512] quantised h (operand layout), [T*8][16] scales
     float *sd;                              // [T][2048] shared-expert output
     float *yp;                              // [T*8][2048] weighted expert outputs

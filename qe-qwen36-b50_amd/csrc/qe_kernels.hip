@@ -170,7 +170,9 @@ __global__ __launch_bounds__(1024) void k_disp_hist(const int32_t *ids, int np, 
 // Dispatch pass 2: offsets and the stable scatter (engine/qe.cpp:1968-1976).
 // Inside a chunk, a pair's rank among earlier same-expert pairs is the count
 // in earlier waves plus its rank in its own wave (8 ballots on the id bits).
-// Block 0 also writes off[] and the work items (expert, first pair, count <= TC).
+// Block 0 also writes off[] and the work items (expert, first pair, count <= TC):
+// those of more than TC / 2 pairs first, n_items[0] items in all, n_items[1] of
+// them big.
 __global__ __launch_bounds__(1024) void k_disp_scatter(const int32_t *ids, int np, const int32_t *chunk_hist, int nch,
                                                        int tc, int32_t *off_out, int32_t *pairs, int4 *items,
                                                        int32_t *n_items) {
@@ -246,7 +248,10 @@ __global__ __launch_bounds__(1024) void k_disp_scatter(const int32_t *ids, int n
             for (int c = 0; c < full; ++c) items[bb + c] = make_int4(tid, s_off[tid] + c * tc, tc, 0);
             if (rem > tc / 2) items[bb + full] = make_int4(tid, s_off[tid] + full * tc, rem, 0);
             if (ns) items[total_b + s_ns[tid] - 1] = make_int4(tid, s_off[tid] + full * tc, rem, 0);
-            if (tid == 255) *n_items = total_b + s_ns[255];
+            if (tid == 255) {
+                n_items[0] = total_b + s_ns[255];
+                n_items[1] = total_b;
+            }
         }
     }
     const int p = blockIdx.x * 1024 + tid;

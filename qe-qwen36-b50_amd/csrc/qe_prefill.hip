@@ -111,6 +111,7 @@ template <bool GU, int NC, int NT> struct TileLds {
 constexpr int qe_cmax(int a, int b) { return a > b ? a : b; }
 template <bool GU> struct ExpertSmem {
     static constexpr int SIZE = qe_cmax(TileLds<GU, 2, 4>::SIZE, qe_cmax(TileLds<GU, 2, 2>::SIZE, TileLds<GU, 2, 1>::SIZE));
+    static_assert(TileLds<GU, 1, 2>::SIZE <= SIZE, "the one-matrix gate/up waves fit as well");
     alignas(16) uint8_t raw[SIZE];
     int pair[QE_MFMA_MC];
 };
@@ -121,10 +122,14 @@ template <bool GU> struct ExpertSmem {
 //   gate/up, NC = 4: h rows 32 (4 yb + wave) + 0..31; groups gate, gate+16, up, up+16;
 //   gate/up, NC = 2: h rows 16 (4 yb + wave) + 0..15; groups gate, up -- a 32-block
 //            of h spans the wave pair (2w, 2w+1), which meets in LDS for its maximum;
+//   gate/up, NC = 1: h rows 32 yb + 16 (wave % 2) + 0..15 of the gate (waves 0, 1) or
+//            up (waves 2, 3) matrix -- half the rows of NC = 2 per workgroup, each
+//            output's K order unchanged; the up waves hand their dots to the gate
+//            waves through LDS;
 //   down:    output rows 64 NC yb + 16 NC wave + 16 c + 0..15.
 template <bool GU, int NC, int NT>
 __device__ __forceinline__ void expert_tile(const GemmTileArgs &a, const int4 it, const int yb, ExpertSmem<GU> &sm) {
-    static_assert(NC == 2 || NC == 4, "two or four column groups per wave");
+    static_assert(NC == 2 || NC == 4 || (GU && NC == 1), "one (gate/up), two or four column groups per wave");
     static_assert(16 * NT <= QE_MFMA_MC, "tiles of the item");
     constexpr int KD = GU ? QE_D : QE_FF_EXP;  // reduction length
     constexpr int NB = KD / 32;                // K blocks
@@ -135,7 +140,8 @@ __device__ __forceinline__ void expert_tile(const GemmTileArgs &a, const int4 it
     auto row_of = [&](int w, int c, int nn) -> int {
         if constexpr (!GU) return yb * (64 * NC) + w * (16 * NC) + 16 * c + nn;
         else if constexpr (NC == 4) return (c < 2 ? 0 : QE_FF_EXP) + (yb * 4 + w) * 32 + 16 * (c & 1) + nn;
-        else return (c == 0 ? 0 : QE_FF_EXP) + (yb * 4 + w) * 16 + nn;
+        else if constexpr (NC == 2) return (c == 0 ? 0 : QE_FF_EXP) + (yb * 4 + w) * 16 + nn;
+        else return (w < 2 ? 0 : QE_FF_EXP) + (yb * 2 + (w & 1)) * 16 + nn;
     };
     const uint8_t *ebase = a.arena + (size_t)it.x * QE_EXPERT_BYTES + (GU ? 0 : QE_EXPERT_DOWN_OFF);
     // Buffer loads: a range-checked resource per operand (reads past the end
@@ -261,8 +267,10 @@ __device__ __forceinline__ void expert_tile(const GemmTileArgs &a, const int4 it
                 if constexpr (NC == 4)
                     asm volatile("v_mov_b32 %0, 0" : "=v"(dep)
                                  : "v"(cw[0][0]), "v"(cw[1][0]), "v"(cw[2][0]), "v"(cw[3][0]));
-                else
+                else if constexpr (NC == 2)
                     asm volatile("v_mov_b32 %0, 0" : "=v"(dep) : "v"(cw[0][0]), "v"(cw[1][0]));
+                else
+                    asm volatile("v_mov_b32 %0, 0" : "=v"(dep) : "v"(cw[0][0]));
                 load_q(nx, qs, dep);
                 __builtin_amdgcn_sched_barrier(0);
             }
@@ -363,6 +371,60 @@ __device__ __forceinline__ void expert_tile(const GemmTileArgs &a, const int4 it
                 }
             }
         }
+    } else if constexpr (GU && NC == 1) {
+        // 32-block yb of h: rows 16 rs + n, rs = wv % 2, from gate wave rs and up wave
+        // 2 + rs.  All of it goes through the stage the last turn did not read.
+        uint8_t *fs = sm.raw + LY::ACT + (NCH & 1) * LY::ACT_SZ;
+        float *utile = (float *)fs;                              // [2][16 NT pairs][16] the up dots
+        float *amax = utile + 2 * 16 * NT * 16;                  // [2][16 NT] |h| maxima per half
+        uint8_t *htile = (uint8_t *)(amax + 2 * 16 * NT);         // [16 NT][32] int8 h, operand order
+        float *stile = (float *)(htile + 16 * NT * 32);          // [16 NT] block scales
+        static_assert((2 * 16 * 16 + 2 * 16 + 32 + 1) * NT * 4 <= LY::ACT_SZ, "the epilogue fits the free stage");
+        const int rs = wv & 1;
+        if (wv >= 2) {
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) utile[(rs * 16 * NT + 16 * t + 4 * g + i) * 16 + n] = acc[0][t][i];
+        }
+        __syncthreads();
+        float h[NT][4], m[NT][4];
+        if (wv < 2) {
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int mi = 16 * t + 4 * g + i;
+                    h[t][i] = silu_mul(acc[0][t][i], utile[(rs * 16 * NT + mi) * 16 + n]);
+                    m[t][i] = max16(fabsf(h[t][i]));
+                    if (n == 0) amax[rs * 16 * NT + mi] = m[t][i];
+                }
+        }
+        __syncthreads();
+        if (wv < 2) {
+            // element 16 rs + n of the block: byte (n / 4) * 16 + (yb % 2) * 8 + n % 4 + 4 rs
+            // of the pair's 64-byte run (yb / 2) of h (the layout of the NC = 2 path);
+            // htile keeps this block's 8-byte groups n / 4 contiguous
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int mi = 16 * t + 4 * g + i;
+                    float d;
+                    const float id = quant_scale_inv(fmaxf(m[t][i], amax[(rs ^ 1) * 16 * NT + mi]), d);
+                    htile[mi * 32 + (n >> 2) * 8 + (n & 3) + 4 * rs] = (uint8_t)quant_one(h[t][i], id);
+                    if (n == 0 && rs == 0) stile[mi] = d;
+                }
+        }
+        __syncthreads();
+        {   // thread (pair tid / 4, 8-byte group tid % 4)
+            const int mi = tid >> 2, q = tid & 3;
+            const int p = mi < 16 * NT ? s_pair[mi] : -1;
+            if (p >= 0) {
+                *(uint2 *)(a.hq + (size_t)p * QE_FF_EXP + (yb >> 1) * 64 + 16 * q + 8 * (yb & 1)) = *(const uint2 *)(htile + mi * 32 + 8 * q);
+                if (q == 0) a.hs[(size_t)p * (QE_FF_EXP / 32) + yb] = stile[mi];
+            }
+        }
     } else if constexpr (GU) {
         // h rows 16 (4 yb + wv) + n: half (wv & 1) of 32-block jb
         const int jb = yb * 2 + (wv >> 1), half = wv & 1;
@@ -423,24 +485,34 @@ __device__ __forceinline__ void expert_tile(const GemmTileArgs &a, const int4 it
     }
 }
 
-// Every item runs NC = 2: gate/up over 8 row groups of 64 h rows, down over 16
-// of 128 output rows.  Workgroup b runs on XCD b % 8 (round-robin dispatch);
-// all row groups of an item run on one XCD, so its activations come from HBM
-// once and from that XCD's L2 after: b = 8 (RG (item / 8) + yb) + item % 8.
-// Big items (33..64 pairs) run NT = 4, small ones NT = 2 or 1.
-template <bool GU> constexpr int expert_rg() { return GU ? QE_FF_EXP / 64 : QE_D / 128; }
+// Gate/up: big items (33..64 pairs, the first n_items[1]) run NT = 4, NC = 2
+// on 8 row groups of 64 h rows; the small ones after them NT = 2 or 1 on
+// NC = 1, 16 row groups of 32 h rows: twice the workgroups of half the life
+// (these items run last, after the big ones, and their workgroups had made the
+// launch's tail).  Workgroup b runs on XCD x = b % 8 (round-robin dispatch) and
+// takes the (b / 8)-th row group of that XCD's items x, x + 8, ..., the big
+// ones' first: all row groups of an item run on one XCD, so its activations
+// come from HBM once and from that XCD's L2 after.  (The odd row groups of a
+// big item as empty workgroups instead, interleaved with its real ones, left
+// half the CUs without work: the dispatcher deals an XCD's workgroups to its
+// CUs in turn.)
+template <bool GU> constexpr int expert_rg() { return GU ? QE_FF_EXP / 32 : QE_D / 128; }
 template <bool GU> QE_DEV void expert_unit(const GemmTileArgs &a, int b, ExpertSmem<GU> &sm) {
-    constexpr int RG = expert_rg<GU>();
-    const int k = b >> 3, item = (k / RG) * 8 + (b & 7), yb = k % RG;
+    static_assert(GU, "the down items run dn_unit");
+    const int x = b & 7, k = b >> 3, nbig = a.n_items[1];
+    const int nbx = nbig > x ? (nbig - x + 7) >> 3 : 0; // big items on this XCD
+    const bool big = k < 8 * nbx;
+    const int k2 = k - 8 * nbx;
+    const int item = x + 8 * (big ? k >> 3 : nbx + (k2 >> 4)), yb = big ? k & 7 : k2 & 15;
     if (item >= a.n_items[0]) return;
     const int4 it = a.items[item];
     static_assert(QE_MFMA_MC == 64, "items of up to four 16-row tiles");
-    if (it.z > 32)
+    if (big)
         expert_tile<GU, 2, 4>(a, it, yb, sm);
     else if (it.z > 16)
-        expert_tile<GU, 2, 2>(a, it, yb, sm);
+        expert_tile<GU, 1, 2>(a, it, yb, sm);
     else
-        expert_tile<GU, 2, 1>(a, it, yb, sm);
+        expert_tile<GU, 1, 1>(a, it, yb, sm);
 }
 // Workgroups over the items of np pairs: an upper bound of the item count
 // (items of more than QE_MFMA_MC / 2 pairs, plus at most one smaller item per

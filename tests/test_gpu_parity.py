@@ -237,8 +237,8 @@ def test_prefill_item_boundaries(ctx, torch_cuda, T):
     # T pairs and the work items take every size class: 16 | 17 (one 16-pair
     # tile | two), 32 | 33 (two tiles | four), 64 | 65 (a full item | plus a
     # one-pair remainder), 130 (two full items and a two-pair remainder).
-    # 2064 | 2081: 32 full items and a 16 | 33-pair remainder through the
-    # large-T gate/up launch (two 1024-thread workgroups per item).
+    # 2064 | 2081: 32 full items and a 16 | 33-pair remainder (the remainder
+    # items on the one-matrix gate/up waves | with the full items).
     torch = torch_cuda
     say(f"prefill item boundaries: 8 experts x {T} pairs")
     bias = np.zeros(256, np.float32)
