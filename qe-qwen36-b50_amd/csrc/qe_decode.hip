@@ -42,6 +42,9 @@
 // being waited for are loaded before the wait.
 #include "qe_kernels.h"
 
+#include <atomic>
+#include <mutex>
+
 #define LD_A(p) __hip_atomic_load((p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
 #define ST_A(p, v) __hip_atomic_store((p), (v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
 #define ADD_A(p, v) __hip_atomic_fetch_add((p), (v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
@@ -1266,21 +1269,37 @@ __global__ __launch_bounds__(NTH) void k_decode(QeDecodeArgs a) {
     }
 }
 
+#define DEC_MAX_DEV 64
+static std::mutex g_dec_setup_mu;
+
+// The grid of each instantiation, per device (the current one): set up on its
+// first launch there, with the kernel's dynamic LDS limit raised for that device.
 template <int TM, bool EXN> static hipError_t launch_decode(const QeDecodeArgs &a, hipStream_t st) {
-    static int grid = 0;
+    static std::atomic<int> grids[DEC_MAX_DEV];
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= DEC_MAX_DEV) return hipErrorInvalidDevice;
+    int grid = grids[dev].load(std::memory_order_acquire);
     if (!grid) {
-        hipError_t e = hipFuncSetAttribute((const void *)k_decode<TM, EXN>, hipFuncAttributeMaxDynamicSharedMemorySize, L_TOTAL);
-        if (e != hipSuccess) return e;
-        int dev = 0, cus = 0, per_cu = 0;
-        if ((e = hipGetDevice(&dev)) != hipSuccess) return e;
-        if ((e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev)) != hipSuccess) return e;
-        if ((e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_decode<TM, EXN>, NTH, L_TOTAL)) != hipSuccess) return e;
-        if (per_cu < 1) return hipErrorInvalidConfiguration;
-        // one workgroup per CU, 64..256 of them (a workgroup's D rows, <= 4 groups
-        // of 8, stay within the 32-row residual buffer); per_cu is 1 (LDS), so the
-        // grid is resident in full on an idle device
-        grid = cus < 256 ? cus : 256;
-        if (grid < DEC_MIN_GRID) return hipErrorInvalidConfiguration;
+        std::lock_guard<std::mutex> lk(g_dec_setup_mu);
+        grid = grids[dev].load(std::memory_order_relaxed);
+        if (!grid) {
+            if ((e = hipFuncSetAttribute((const void *)k_decode<TM, EXN>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                         L_TOTAL)) != hipSuccess)
+                return e;
+            int cus = 0, per_cu = 0;
+            if ((e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev)) != hipSuccess) return e;
+            if ((e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_decode<TM, EXN>, NTH, L_TOTAL)) != hipSuccess)
+                return e;
+            if (per_cu < 1) return hipErrorInvalidConfiguration;
+            // one workgroup per CU, 64..256 of them (a workgroup's D rows, <= 4 groups
+            // of 8, stay within the 32-row residual buffer); per_cu is 1 (LDS), so the
+            // grid is resident in full on an idle device
+            grid = cus < 256 ? cus : 256;
+            if (grid < DEC_MIN_GRID) return hipErrorInvalidConfiguration;
+            grids[dev].store(grid, std::memory_order_release);
+        }
     }
     void *args[] = {(void *)&a};
     return hipLaunchKernel((const void *)k_decode<TM, EXN>, dim3(grid), dim3(NTH), args, L_TOTAL, st);
