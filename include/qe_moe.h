@@ -57,8 +57,9 @@ size_t qe_moe_expert_bytes(void);
 
 /* Copy n_experts blobs (expert ids first..first+n-1 of `layer`) into the arena,
  * from host (src_on_device = 0) or device memory.  A pack's blk.N.experts
- * entry (engine/qconv.cpp:202-228) copies in as is.  Replaces the arena/host
- * expert copies of engine/qe.cpp:1172-1194. */
+ * entry (engine/qconv.cpp:202-228) copies in as is.  A host source is copied
+ * before the call returns; a device source is copied in `stream` order.
+ * Replaces the arena/host expert copies of engine/qe.cpp:1172-1194. */
 int qe_moe_upload_experts(qe_moe_ctx *ctx, int layer, int first, int n_experts, const void *src, int src_on_device,
                           void *stream);
 
@@ -68,7 +69,8 @@ int qe_moe_upload_experts(qe_moe_ctx *ctx, int layer, int first, int n_experts, 
  * builds it at :1055); bias fp32[256] added to logits 0..255 (NULL = none);
  * sh_gu Q8 [1024 rows x 2048] (gate rows 0..511, up rows 512..1023);
  * sh_down Q8 [2048 rows x 512].  Any pointer may be NULL to keep the current
- * contents.  Sources are host or device memory per src_on_device. */
+ * contents.  Sources are host or device memory per src_on_device; host
+ * sources are copied before the call returns. */
 int qe_moe_set_dense(qe_moe_ctx *ctx, int layer, const float *post_norm, const float *router, const float *bias,
                      const void *sh_gu, const void *sh_down, int src_on_device, void *stream);
 

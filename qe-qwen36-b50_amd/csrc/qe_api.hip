@@ -231,6 +231,7 @@ int qe_moe_upload_experts(qe_moe_ctx *c, int layer, int first, int n, const void
     uint8_t *dst = c->arena + (size_t)layer * QE_LAYER_EXPERT_BYTES + (size_t)first * QE_EXPERT_BYTES;
     HIP_TRY(hipMemcpyAsync(dst, src, (size_t)n * QE_EXPERT_BYTES, on_dev ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice,
                            (hipStream_t)stream));
+    if (!on_dev) HIP_TRY(hipStreamSynchronize((hipStream_t)stream)); /* host sources need not outlive the call */
     mark_experts(c, layer, first, n);
     return QE_OK;
 }
