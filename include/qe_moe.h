@@ -36,8 +36,8 @@ extern "C" {
 #define QE_ERR_ARG (-1)   /* bad argument (null pointer, layer or T out of range) */
 #define QE_ERR_HIP (-2)   /* a HIP runtime call failed */
 #define QE_ERR_OOM (-3)   /* device allocation failed */
-#define QE_ERR_STATE (-4) /* layer not ready (a weight tensor or expert never set), or an earlier decode
-                              launch timed out in an exchange poll (see qe_moe_check) */
+#define QE_ERR_STATE (-4) /* layer not ready (a weight tensor or expert never set), or an earlier launch
+                              timed out in a bounded wait (see qe_moe_check) */
 
 typedef struct qe_moe_ctx qe_moe_ctx;
 
@@ -206,9 +206,11 @@ int qe_moe_synth_x(uint64_t seed, int inst, float *dev_out, int64_t n, void *str
  * (3, 4).  Host only, no device work. */
 int qe_moe_synth_zipf_bias(uint64_t seed, int layer, double s, float *out);
 
-/* Decode poll timeouts.  The T <= 8 path synchronises workgroups through
- * bounded polls; a poll that gives up (a hung or starved peer) lets the
- * launch finish with invalid outputs and records it in a host-visible word.
+/* Poll timeouts.  The T <= 8 path synchronises workgroups through bounded
+ * polls, and so do the down workgroups of the fused prefill launch (32..4095
+ * tokens) waiting for their item's gate/up workgroups; a wait that gives up (a
+ * hung or starved peer) lets the launch finish with invalid outputs and
+ * records it in a host-visible word.
  * The next call that looks reports each such launch once as QE_ERR_STATE:
  * every forward entry point checks at entry (without synchronising, so a
  * launch still running is reported by a later call), and qe_moe_get_routing,
@@ -219,10 +221,15 @@ int qe_moe_check(qe_moe_ctx *ctx, void *stream);
 /* Test hooks, no reference counterpart.  qe_moe_debug_set_epoch writes the
  * decode launch counter (its low 16 bits tag the exchanged words), so a test
  * can run launches across the counter's wrap; qe_moe_debug_set_spin_cap sets
- * the reads an exchange poll makes before giving up (0 = the default), so a
- * test can force a timeout without a stalled kernel. */
+ * the reads an exchange poll (decode) or a down workgroup's wait for its item
+ * (the fused prefill launch, 32..4095 tokens) makes before giving up (0 = the
+ * default), so a test can force a timeout without a stalled kernel. */
 int qe_moe_debug_set_epoch(qe_moe_ctx *ctx, uint32_t epoch, void *stream);
 int qe_moe_debug_set_spin_cap(qe_moe_ctx *ctx, int cap);
+/* Test hook, no reference counterpart: the fused prefill launch's down
+ * workgroups wait for `extra` more gate/up workgroups than their item has (0 =
+ * as in use), so that every such wait gives up after the spin cap. */
+int qe_moe_debug_fused_wait_extra(qe_moe_ctx *ctx, int extra);
 
 const char *qe_moe_last_error(void);
 

@@ -52,6 +52,7 @@ struct qe_moe_ctx {
     unsigned *err_host = nullptr; // pinned, host-mapped: 0, or 1 + epoch of the last decode launch whose poll timed out
     unsigned *err_dev = nullptr;  // the same word as the kernels address it
     unsigned err_seen = 0;        // the value last reported
+    unsigned prefill_seq = 0;     // prefill calls so far: a timed-out wait of one stores 0x80000000 | its number
     int spin_cap = QE_DECODE_SPIN_CAP;
     float *pingpong[2] = {nullptr, nullptr};
     std::vector<void *> allocs;
@@ -101,6 +102,9 @@ static int take_decode_error(qe_moe_ctx *c, const char *where) {
     const unsigned v = __atomic_load_n(c->err_host, __ATOMIC_ACQUIRE);
     if (!v || v == c->err_seen) return QE_OK;
     c->err_seen = v;
+    if (v & 0x80000000u)
+        return fail(QE_ERR_STATE, "%s: prefill call %u timed out waiting for its gate/up workgroups; its outputs are invalid",
+                    where, v & 0x7fffffffu);
     return fail(QE_ERR_STATE, "%s: the decode launch of epoch %u timed out waiting for an exchange; its outputs are invalid",
                 where, v - 1u);
 }
@@ -166,6 +170,7 @@ int qe_moe_create(int device, int n_layers, int t_max, qe_moe_ctx **out) {
     A(S.sd, T * QE_D * 4);
     A(S.yp, NP * QE_D * 4);
     A(S.chunk_hist, nch * QE_N_EXPERT * 4);
+    A(S.item_done, max_items * 4);
     A(c->bias_on, L);
     A(c->ex, (size_t)QE_DECODE_EX_WORDS * 8);
     A(c->sync, QE_DECODE_SYNC_WORDS * 4);
@@ -186,6 +191,7 @@ int qe_moe_create(int device, int n_layers, int t_max, qe_moe_ctx **out) {
         else {
             c->err_dev = (unsigned *)d;
             memset(h, 0, 256);
+            S.err = c->err_dev;
         }
     }
     if (rc != QE_OK) {
@@ -195,6 +201,7 @@ int qe_moe_create(int device, int n_layers, int t_max, qe_moe_ctx **out) {
     }
     S.t_max = t_max;
     S.prof = &c->prof;
+    S.spin_cap = c->spin_cap;
     if (hipMemset(c->bias, 0, L * QE_N_EXPERT * 4) != hipSuccess ||
         hipMemset(c->bias_on, 0, L) != hipSuccess || hipMemset(c->sync, 0, QE_DECODE_SYNC_WORDS * 4) != hipSuccess ||
         hipMemset(c->ex, 0, (size_t)QE_DECODE_EX_WORDS * 8) != hipSuccess ||
@@ -403,7 +410,10 @@ int qe_moe_forward(qe_moe_ctx *c, int layer, const float *x2, float *x, int T, v
     if (rc) return rc;
     HIP_TRY(hipSetDevice(c->device));
     if (T <= QE_SMALL_T) HIP_TRY(run_decode(c, layer, 1, x2, x, T, true, (hipStream_t)stream));
-    else HIP_TRY(qe_launch_layer(layer_ptrs(c, layer), c->S, x2, true, x2, x, T, (hipStream_t)stream));
+    else {
+        c->S.err_val = 0x80000000u | (++c->prefill_seq & 0x7fffffffu);
+        HIP_TRY(qe_launch_layer(layer_ptrs(c, layer), c->S, x2, true, x2, x, T, (hipStream_t)stream));
+    }
     return QE_OK;
 }
 
@@ -416,8 +426,10 @@ int qe_moe_forward_norm(qe_moe_ctx *c, int layer, const float *x2, float *x, int
     HIP_TRY(hipSetDevice(c->device));
     if (T <= QE_SMALL_T)
         HIP_TRY(run_decode(c, layer, 1, x2, x, T, true, (hipStream_t)stream, next_norm, xn));
-    else
+    else {
+        c->S.err_val = 0x80000000u | (++c->prefill_seq & 0x7fffffffu);
         HIP_TRY(qe_launch_layer(layer_ptrs(c, layer), c->S, x2, true, x2, x, T, (hipStream_t)stream, next_norm, xn));
+    }
     return QE_OK;
 }
 
@@ -426,7 +438,10 @@ int qe_moe_forward_normed(qe_moe_ctx *c, int layer, const float *xn, float *y, i
     if (rc) return rc;
     HIP_TRY(hipSetDevice(c->device));
     if (T <= QE_SMALL_T) HIP_TRY(run_decode(c, layer, 1, xn, y, T, false, (hipStream_t)stream));
-    else HIP_TRY(qe_launch_layer(layer_ptrs(c, layer), c->S, xn, false, nullptr, y, T, (hipStream_t)stream));
+    else {
+        c->S.err_val = 0x80000000u | (++c->prefill_seq & 0x7fffffffu);
+        HIP_TRY(qe_launch_layer(layer_ptrs(c, layer), c->S, xn, false, nullptr, y, T, (hipStream_t)stream));
+    }
     return QE_OK;
 }
 
@@ -512,9 +527,16 @@ int qe_moe_debug_set_epoch(qe_moe_ctx *c, uint32_t epoch, void *stream) {
     return QE_OK;
 }
 
+int qe_moe_debug_fused_wait_extra(qe_moe_ctx *c, int extra) {
+    if (!c || extra < 0) return fail(QE_ERR_ARG, "debug_fused_wait_extra: bad argument");
+    c->S.wait_extra = extra;
+    return QE_OK;
+}
+
 int qe_moe_debug_set_spin_cap(qe_moe_ctx *c, int cap) {
     if (!c || cap < 0) return fail(QE_ERR_ARG, "debug_set_spin_cap: bad argument");
     c->spin_cap = cap > 0 ? cap : QE_DECODE_SPIN_CAP;
+    c->S.spin_cap = c->spin_cap;
     return QE_OK;
 }
 

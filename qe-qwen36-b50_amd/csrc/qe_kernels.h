@@ -62,6 +62,10 @@ struct QeScratch {
     float *sd;                              // [T][2048] shared-expert output
     float *yp;                              // [T*8][2048] weighted expert outputs
     int32_t *chunk_hist;                    // [T*8/1024][256]
+    int32_t *item_done;                     // [max items] finished gate/up workgroups per item (fused launch)
+    unsigned *err; unsigned err_val;        // a fused launch's wait that gave up stores err_val to *err
+    int spin_cap;                           // reads such a wait may take
+    int wait_extra;                         // test hook: gate/up workgroups a fused down wait expects beyond its item's
     int t_max;
     QeProf *prof;                           // host-side timing, may be nullptr
 };

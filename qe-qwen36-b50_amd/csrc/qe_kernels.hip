@@ -175,7 +175,7 @@ __global__ __launch_bounds__(1024) void k_disp_hist(const int32_t *ids, int np, 
 // them big.
 __global__ __launch_bounds__(1024) void k_disp_scatter(const int32_t *ids, int np, const int32_t *chunk_hist, int nch,
                                                        int tc, int32_t *off_out, int32_t *pairs, int4 *items,
-                                                       int32_t *n_items) {
+                                                       int32_t *n_items, int32_t *item_done) {
     __shared__ int s_before[QE_N_EXPERT], s_off[QE_N_EXPERT], s_cnt[QE_N_EXPERT], s_scan[QE_N_EXPERT];
     __shared__ int s_w[16][QE_N_EXPERT];
     __shared__ int s_part[2][4][QE_N_EXPERT];
@@ -252,6 +252,8 @@ __global__ __launch_bounds__(1024) void k_disp_scatter(const int32_t *ids, int n
                 n_items[0] = total_b + s_ns[255];
                 n_items[1] = total_b;
             }
+            if (item_done) // the fused gate/up + down launch counts its gate/up workgroups per item
+                for (int i = tid; i < total_b + s_ns[255]; i += 256) item_done[i] = 0;
         }
     }
     const int p = blockIdx.x * 1024 + tid;
@@ -402,7 +404,7 @@ hipError_t qe_launch_layer(const QeLayerPtrs &L, const QeScratch &S, const float
         QE_PROF(QP_DISPATCH); // the histogram came with k_topk
         const int np = T * QE_K_USED, nch = (np + 1023) / 1024;
         k_disp_scatter<<<nch, 1024, 0, st>>>(S.ids, np, S.chunk_hist, nch, QE_MFMA_MC, S.off, S.pairs, S.items,
-                                              S.n_items);
+                                              S.n_items, S.item_done);
     }
     {
         QE_PROF(QP_GU); // routed gate/up, then routed down + shared down
@@ -423,7 +425,7 @@ hipError_t qe_launch_dispatch(const QeScratch &S, int T, hipStream_t st) {
     const int np = T * QE_K_USED, nch = (np + 1023) / 1024;
     k_disp_hist<<<nch, 1024, 0, st>>>(S.ids, np, S.chunk_hist);
     k_disp_scatter<<<nch, 1024, 0, st>>>(S.ids, np, S.chunk_hist, nch, QE_MFMA_MC, S.off, S.pairs, S.items,
-                                          S.n_items);
+                                          S.n_items, nullptr);
     return hipGetLastError();
 }
 
@@ -479,7 +481,7 @@ hipError_t qe_launch_dispatch_noalloc(const int32_t *ids, int T, int32_t *off, i
     int32_t *n_items = (int32_t *)(base + NOALLOC_HIST_BYTES + (size_t)NOALLOC_ITEMS * 16);
     const int np = T * QE_K_USED, nch = (np + 1023) / 1024;
     k_disp_hist<<<nch, 1024, 0, st>>>(ids, np, chunk_hist);
-    k_disp_scatter<<<nch, 1024, 0, st>>>(ids, np, chunk_hist, nch, QE_MFMA_MC, off, pairs, items, n_items);
+    k_disp_scatter<<<nch, 1024, 0, st>>>(ids, np, chunk_hist, nch, QE_MFMA_MC, off, pairs, items, n_items, nullptr);
     return hipGetLastError();
 }
 

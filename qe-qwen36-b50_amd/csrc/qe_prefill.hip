@@ -61,7 +61,32 @@ struct GemmTileArgs {
     int8_t *hq; float *hs;     // gate/up output: quantised h (operand layout) + block scales
     float *yp;                 // down output
     int dn_rgw;                // down: row groups of 128 output rows per workgroup (1, 2 or 4)
+    int32_t *item_done;        // fused gate/up + down launch: gate/up workgroups done per item (else nullptr)
+    unsigned *err;             // fused launch: where a down workgroup's wait that gave up is recorded
+    unsigned err_val;          //   (the value it stores there)
+    int spin_cap;              //   and the reads a wait may take
+    int wait_extra;            //   test hook: more gate/up workgroups than the item has (0 in use)
 };
+
+// Stores and loads through to the device coherence point (sc1): the h of a gate/up
+// workgroup is read by down workgroups of the same launch in the fused form, on
+// whatever XCD they run, with no L2 write-back or invalidation between them.
+typedef unsigned qe_st_u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned qe_st_u32x2 __attribute__((ext_vector_type(2)));
+QE_DEV void st_sc1(void *p, uint4 v) {
+    const qe_st_u32x4 w = {v.x, v.y, v.z, v.w};
+    asm volatile("global_store_dwordx4 %0, %1, off sc1" ::"v"(p), "v"(w) : "memory");
+}
+QE_DEV void st_sc1(void *p, uint2 v) {
+    const qe_st_u32x2 w = {v.x, v.y};
+    asm volatile("global_store_dwordx2 %0, %1, off sc1" ::"v"(p), "v"(w) : "memory");
+}
+QE_DEV void st_sc1(void *p, float v) { asm volatile("global_store_dword %0, %1, off sc1" ::"v"(p), "v"(v) : "memory"); }
+QE_DEV float4 ld_sc1_f4(const void *p) {
+    qe_st_u32x4 w;
+    asm volatile("global_load_dwordx4 %0, %1, off sc1\n\ts_waitcnt vmcnt(0)" : "=v"(w) : "v"(p) : "memory");
+    return make_float4(__uint_as_float(w.x), __uint_as_float(w.y), __uint_as_float(w.z), __uint_as_float(w.w));
+}
 
 // v_mfma_i32_16x16x32_i8 with one 32-element block per instruction keeps the
 // block dot an exact int32; lane l supplies k = 8 (l / 16) + 0..7 of row / column
@@ -421,8 +446,15 @@ __device__ __forceinline__ void expert_tile(const GemmTileArgs &a, const int4 it
             const int mi = tid >> 2, q = tid & 3;
             const int p = mi < 16 * NT ? s_pair[mi] : -1;
             if (p >= 0) {
-                *(uint2 *)(a.hq + (size_t)p * QE_FF_EXP + (yb >> 1) * 64 + 16 * q + 8 * (yb & 1)) = *(const uint2 *)(htile + mi * 32 + 8 * q);
-                if (q == 0) a.hs[(size_t)p * (QE_FF_EXP / 32) + yb] = stile[mi];
+                int8_t *hp = a.hq + (size_t)p * QE_FF_EXP + (yb >> 1) * 64 + 16 * q + 8 * (yb & 1);
+                float *sp = a.hs + (size_t)p * (QE_FF_EXP / 32) + yb;
+                if (a.item_done) { // fused launch: written through for its down workgroups
+                    st_sc1(hp, *(const uint2 *)(htile + mi * 32 + 8 * q));
+                    if (q == 0) st_sc1(sp, stile[mi]);
+                } else {
+                    *(uint2 *)hp = *(const uint2 *)(htile + mi * 32 + 8 * q);
+                    if (q == 0) *sp = stile[mi];
+                }
             }
         }
     } else if constexpr (GU) {
@@ -465,8 +497,15 @@ __device__ __forceinline__ void expert_tile(const GemmTileArgs &a, const int4 it
             const int mi = tid >> 2, q = tid & 3;
             const int p = mi < 16 * NT ? s_pair[mi] : -1;
             if (p >= 0) {
-                *(uint4 *)(a.hq + (size_t)p * QE_FF_EXP + (jb >> 1) * 64 + 16 * q) = *(const uint4 *)(htile + mi * 64 + 16 * q);
-                if (q == 0) *(float2 *)(a.hs + (size_t)p * (QE_FF_EXP / 32) + 2 * (jb >> 1)) = *(const float2 *)(stile + mi * 2);
+                int8_t *hp = a.hq + (size_t)p * QE_FF_EXP + (jb >> 1) * 64 + 16 * q;
+                float *sp = a.hs + (size_t)p * (QE_FF_EXP / 32) + 2 * (jb >> 1);
+                if (a.item_done) { // fused launch: written through for its down workgroups
+                    st_sc1(hp, *(const uint4 *)(htile + mi * 64 + 16 * q));
+                    if (q == 0) st_sc1(sp, *(const uint2 *)(stile + mi * 2));
+                } else {
+                    *(uint4 *)hp = *(const uint4 *)(htile + mi * 64 + 16 * q);
+                    if (q == 0) *(float2 *)sp = *(const float2 *)(stile + mi * 2);
+                }
             }
         }
     } else {
@@ -513,6 +552,13 @@ template <bool GU> QE_DEV void expert_unit(const GemmTileArgs &a, int b, ExpertS
         expert_tile<GU, 1, 2>(a, it, yb, sm);
     else
         expert_tile<GU, 1, 1>(a, it, yb, sm);
+    if (a.item_done) {
+        // fused launch: every thread's h stores (sc1, written through) are acknowledged
+        // before the item's count of finished gate/up workgroups goes up
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (threadIdx.x == 0) __hip_atomic_fetch_add(a.item_done + item, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
 }
 // Workgroups over the items of np pairs: an upper bound of the item count
 // (items of more than QE_MFMA_MC / 2 pairs, plus at most one smaller item per
@@ -981,7 +1027,7 @@ struct DnSmem {
     float w[QE_MFMA_MC];                            // pair weights
     int pair[QE_MFMA_MC];
 };
-template <int NT>
+template <int NT, bool FUSED>
 __device__ __forceinline__ void dn_tile(const GemmTileArgs &a, const int4 it, const int rg0, const int nrg, DnSmem &sm) {
     constexpr int NC = 2;
     constexpr uint32_t RB = QE_DN_ROW_BYTES;
@@ -1021,7 +1067,8 @@ __device__ __forceinline__ void dn_tile(const GemmTileArgs &a, const int4 it, co
             const uint32_t src = (uint32_t)(pm < 0 ? sm.pair[0] : pm) * QE_FF_EXP + 16 * (tid & 15);
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
-                const qe_u32x4 t4 = __builtin_amdgcn_raw_buffer_load_b128(ar, src, 256 * h, 0);
+                // fused launch: h of this launch's gate/up workgroups, from the coherence point (sc1)
+                const qe_u32x4 t4 = __builtin_amdgcn_raw_buffer_load_b128(ar, src, 256 * h, FUSED ? 16 : 0);
                 v[r][h] = make_uint4(t4.x, t4.y, t4.z, t4.w);
             }
         }
@@ -1030,7 +1077,10 @@ __device__ __forceinline__ void dn_tile(const GemmTileArgs &a, const int4 it, co
         const int sm_m = tid >> 2;
         if (sc_role) {
             const int pm = sm.pair[sm_m];
-            if (pm >= 0) sc = ((const float4 *)(a.as + (size_t)pm * (QE_FF_EXP / 32)))[tid & 3];
+            if (pm >= 0) {
+                const float4 *sp = (const float4 *)(a.as + (size_t)pm * (QE_FF_EXP / 32)) + (tid & 3);
+                sc = FUSED ? ld_sc1_f4(sp) : *sp;
+            }
         }
 #pragma unroll
         for (int r = 0; r < NT; ++r) {
@@ -1158,18 +1208,37 @@ __device__ __forceinline__ void dn_tile(const GemmTileArgs &a, const int4 it, co
 
 // Down workgroup b: item and row-group block; all row-group blocks of an item
 // on one XCD (b % 8), as for gate/up.  Big items run NT = 4, smaller NT = 2, 1.
+template <bool FUSED> __device__ __forceinline__ void dn_unit_at(const GemmTileArgs &a, int item, int rgb, DnSmem &sm) {
+    const int4 it = a.items[item];
+    static_assert(QE_MFMA_MC == 64, "items of up to four 16-row tiles");
+    if constexpr (FUSED) {
+        // the item's gate/up workgroups (8 row groups of a big item, 16 of a small one)
+        // come earlier in the grid, so all have started; a bounded wait all the same
+        if (threadIdx.x == 0) {
+            const int need = (it.z > QE_MFMA_MC / 2 ? 8 : 16) + a.wait_extra;
+            for (int spins = 0;; ++spins) {
+                if (__hip_atomic_load(a.item_done + item, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= need) break;
+                if (spins + 1 >= a.spin_cap) {
+                    __hip_atomic_store(a.err, a.err_val, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(2);
+            }
+        }
+        __syncthreads();
+    }
+    if (it.z > 32)
+        dn_tile<4, FUSED>(a, it, rgb * a.dn_rgw, a.dn_rgw, sm);
+    else if (it.z > 16)
+        dn_tile<2, FUSED>(a, it, rgb * a.dn_rgw, a.dn_rgw, sm);
+    else
+        dn_tile<1, FUSED>(a, it, rgb * a.dn_rgw, a.dn_rgw, sm);
+}
 __device__ __forceinline__ void dn_unit(const GemmTileArgs &a, int b, DnSmem &sm) {
     const int rgb_n = (QE_D / 128) / a.dn_rgw; // row-group blocks per item
     const int k = b >> 3, item = (k / rgb_n) * 8 + (b & 7), rgb = k % rgb_n;
     if (item >= a.n_items[0]) return;
-    const int4 it = a.items[item];
-    static_assert(QE_MFMA_MC == 64, "items of up to four 16-row tiles");
-    if (it.z > 32)
-        dn_tile<4>(a, it, rgb * a.dn_rgw, a.dn_rgw, sm);
-    else if (it.z > 16)
-        dn_tile<2>(a, it, rgb * a.dn_rgw, a.dn_rgw, sm);
-    else
-        dn_tile<1>(a, it, rgb * a.dn_rgw, a.dn_rgw, sm);
+    dn_unit_at<false>(a, item, rgb, sm);
 }
 // workgroups of the routed down over the items of np pairs (as expert_max_wg)
 QE_HD int dn_max_wg(int np, int rgw) { return ((QE_D / 128) / rgw) * (((np / (QE_MFMA_MC / 2 + 1) + 1 + QE_N_EXPERT) + 7) & ~7); }
@@ -1196,6 +1265,50 @@ __global__ __launch_bounds__(256, 2) void k_expert_dn(GemmTileArgs a, int nr, co
     }
 }
 
+// From QE_FUSE_T_MIN to QE_FUSE_T tokens the routed gate/up, the routed down and
+// the shared down run as one launch: the down workgroups alone would leave CUs
+// idle, and the gate/up work ends in a tail of small items.  Workgroup b runs on XCD x = b % 8
+// and is the (b / 8)-th of that XCD's sequence, laid out from the item counts:
+// its items' gate/up workgroups (as k_expert_gu), the shared down tiles of the
+// XCD (they wait for nothing), its items' down workgroups (big items first),
+// then nothing (the grid is an upper bound).  A down workgroup waits until its
+// item's gate/up workgroups have counted themselves done (their h written
+// through, sc1, and acknowledged first) and stages h from the coherence point.
+// The dispatcher starts an XCD's workgroups in grid order, so every gate/up
+// workgroup a down one waits for has started.
+#ifndef QE_FUSE_T_MIN
+#define QE_FUSE_T_MIN 32
+#endif
+#ifndef QE_FUSE_T
+#define QE_FUSE_T 4096
+#endif
+__global__ __launch_bounds__(256, 2) void k_expert_gudn(GemmTileArgs gu, GemmTileArgs dn, int nshx,
+                                                        const _Float16 *hhl, int T, const uint8_t *Wsd, float *sd) {
+    __shared__ union {
+        ExpertSmem<true> g;
+        DnSmem d;
+        Shdn64Lds s;
+    } sm;
+    const int b = blockIdx.x, x = b & 7, k = b >> 3;
+    const int ni = gu.n_items[0], nb = gu.n_items[1];
+    const int nix = ni > x ? (ni - x + 7) >> 3 : 0, nbx = nb > x ? (nb - x + 7) >> 3 : 0; // items x, x + 8, ..
+    const int gux = 8 * nbx + 16 * (nix - nbx);
+    if (k < gux) {
+        expert_unit<true>(gu, b, sm.g);
+        return;
+    }
+    int r = k - gux;
+    if (r < nshx) { // shared tile s = 8 r + x: the 16 column tiles of one 64-token pair back to back
+        const int mp = 8 * (r / (QE_D / 128)) + x;
+        if (mp >= (T + 63) / 64) return;
+        shdn_tile64(hhl, T, Wsd, sd, mp, r % (QE_D / 128), (uint8_t *)&sm.s);
+        return;
+    }
+    r -= nshx;
+    const int rgb_n = (QE_D / 128) / dn.dn_rgw;
+    if (r < nix * rgb_n) dn_unit_at<true>(dn, x + 8 * (r / rgb_n), r % rgb_n, sm.d);
+}
+
 hipError_t qe_launch_router_shgu(const QeLayerPtrs &L, const QeScratch &S, int T, hipStream_t st) {
     const int nr = RS_NT * ((T + 63) / 64) * RT_SPLIT, ns = 8 * RS_JT * (((T + 31) / 32 + 7) / 8);
     if (T >= QE_RS_SPLIT_T) {
@@ -1218,13 +1331,28 @@ hipError_t qe_launch_expert_mfma(const QeLayerPtrs &L, const QeScratch &S, int T
     GemmTileArgs g{};
     g.arena = L.arena; g.pairs = S.pairs; g.items = S.items; g.n_items = S.n_items; g.wts = S.wts;
     g.aq = S.xqp; g.a_bytes = T * QE_D; g.as = S.xs; g.a_row_div = QE_K_USED; g.hq = S.hqp; g.hs = S.hs;
-    k_expert_gu<<<expert_max_wg<true>(np), 256, 0, st>>>(g);
-    g.aq = S.hqp; g.a_bytes = np * QE_FF_EXP; g.as = S.hs; g.a_row_div = 1; g.yp = S.yp;
+    const bool fused = T >= QE_FUSE_T_MIN && T < QE_FUSE_T && S.item_done;
+    if (fused) {
+        g.item_done = S.item_done; g.err = S.err; g.err_val = S.err_val; g.spin_cap = S.spin_cap;
+        g.wait_extra = S.wait_extra;
+    } else {
+        k_expert_gu<<<expert_max_wg<true>(np), 256, 0, st>>>(g);
+    }
+    GemmTileArgs d = g;
+    d.aq = S.hqp; d.a_bytes = np * QE_FF_EXP; d.as = S.hs; d.a_row_div = 1; d.yp = S.yp;
     // row groups per down workgroup: fewer, longer workgroups where the items
     // alone fill the CUs several times over
-    g.dn_rgw = T >= QE_DN_RGW4_T ? 4 : T >= QE_DN_RGW2_T ? 2 : 1; // 4 from 256 tokens: measured best at 512 and 8192
+    // (4 from 256 tokens in separate launches: measured best at 512 and 8192; fused,
+    // shorter down workgroups drain the tail sooner: 1 below 512 tokens, then 2)
+    d.dn_rgw = fused ? (T < 512 ? 1 : 2) : T >= QE_DN_RGW4_T ? 4 : T >= QE_DN_RGW2_T ? 2 : 1;
     const int nsh = 8 * (QE_D / 128) * (((T + 63) / 64 + 7) / 8);
-    const int nr = dn_max_wg(np, g.dn_rgw); // a multiple of 8: shared tiles start on XCD 0
-    k_expert_dn<<<nr + nsh, 256, 0, st>>>(g, nr, (const _Float16 *)S.shgu, T, L.sh_dn, S.sd);
+    const int nr = dn_max_wg(np, d.dn_rgw); // a multiple of 8: shared tiles start on XCD 0
+    if (fused) {
+        // per XCD at most: 16 gate/up and rgb_n down workgroups for each of its items, and its shared tiles
+        const int ix = ((np / (QE_MFMA_MC / 2 + 1) + 1 + QE_N_EXPERT) + 7) / 8, rgb_n = (QE_D / 128) / d.dn_rgw;
+        k_expert_gudn<<<8 * ((16 + rgb_n) * ix + nsh / 8), 256, 0, st>>>(g, d, nsh / 8, (const _Float16 *)S.shgu, T,
+                                                                          L.sh_dn, S.sd);
+    } else
+        k_expert_dn<<<nr + nsh, 256, 0, st>>>(d, nr, (const _Float16 *)S.shgu, T, L.sh_dn, S.sd);
     return hipGetLastError();
 }

@@ -95,6 +95,7 @@ def load(path: str = LIB_PATH):
         "qe_moe_dispatch_noalloc": (i32, [vp, i32, vp, vp, vp]),
         "qe_moe_debug_set_epoch": (i32, [vp, ctypes.c_uint32, vp]),
         "qe_moe_debug_set_spin_cap": (i32, [vp, i32]),
+        "qe_moe_debug_fused_wait_extra": (i32, [vp, i32]),
     }
     for name, (res, args) in sig.items():
         f = getattr(lib, name)
@@ -204,7 +205,8 @@ class MoE:
         return dict(ids=ids, wts=wts, shg=shg, off=off, pairs=pairs, sd=sd)
 
     def check(self, stream=None):
-        """Synchronise `stream`; raise QeError if a decode launch timed out in an exchange poll."""
+        """Synchronise `stream`; raise QeError if a decode launch timed out in an exchange poll, or a fused
+        prefill launch in a down workgroup's wait."""
         _check(_lib.qe_moe_check(self.h, _stream(stream)))
 
     def debug_set_epoch(self, epoch, stream=None):
@@ -212,6 +214,9 @@ class MoE:
 
     def debug_set_spin_cap(self, cap):
         _check(_lib.qe_moe_debug_set_spin_cap(self.h, cap))
+
+    def debug_fused_wait_extra(self, extra):
+        _check(_lib.qe_moe_debug_fused_wait_extra(self.h, extra))
 
     def dispatch(self, ids_dev, T, stream=None):
         _check(_lib.qe_moe_dispatch(self.h, _ptr(ids_dev), T, _stream(stream)))

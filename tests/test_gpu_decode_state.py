@@ -113,6 +113,50 @@ def test_decode_poll_timeout_is_reported(torch_cuda):
         m.close()
 
 
+def test_fused_prefill_wait_timeout_is_reported(torch_cuda):
+    # From 32 to 4095 tokens the routed gate/up, routed down and shared down run as
+    # one launch whose down workgroups wait for their item's gate/up workgroups.
+    # The grid order usually finds those done at the first read, so the test hook
+    # makes every wait expect one workgroup more than exists, and a cap of one read
+    # lets each give up at once (the kernel still runs to its end); the next call
+    # reports it, once, with the prefill call's number.  Then the hook and the cap
+    # back to their defaults, and the output checked against the oracle.
+    torch = torch_cuda
+    T = 512
+    m = qe_moe.MoE(n_layers=1, t_max=T)
+    try:
+        L = O.SynthLayer(SEED, 0)
+        m.synth_layer(0, SEED, None)
+        x = O.gen_x(SEED, 7, T)
+        xd = torch.from_numpy(x).cuda()
+        y = torch.empty_like(xd)
+        m.debug_set_spin_cap(1)
+        m.debug_fused_wait_extra(1)
+        say("fused prefill wait: forced by the wait hook and a one-read cap, T=512")
+        err = None
+        for _ in range(5):
+            m.forward_normed(0, xd, y, T)
+            try:
+                m.check()
+            except qe_moe.QeError as ex:
+                err = ex
+                break
+        assert err is not None and err.code == qe_moe.QE_ERR_STATE and "prefill call" in str(err)
+        m.check()  # reported once, then cleared
+        m.debug_fused_wait_extra(0)
+        m.debug_set_spin_cap(0)
+        m.forward_normed(0, xd, y, T)
+        m.check()
+        o = O.moe_layer(L, x)
+        g = m.routing(T)
+        assert np.array_equal(g["ids"], o["ids"])
+        e = float(np.linalg.norm(y.cpu().numpy().astype(np.float64) - o["out"]) / np.linalg.norm(o["out"]))
+        say(f"  default cap again: out rel-L2 {e:.2e}")
+        assert e <= 1e-3
+    finally:
+        m.close()
+
+
 def test_layer_readiness(torch_cuda):
     torch = torch_cuda
     m = qe_moe.MoE(n_layers=1, t_max=8)
