@@ -132,6 +132,16 @@ QE_DEV float max16(float v) {
     v = fmaxf(v, dpp_f<QE_DPP_HMIRROR>(v));
     return fmaxf(v, dpp_f<QE_DPP_MIRROR>(v));
 }
+// |v| maximum within aligned groups of 16 lanes, on the bit patterns: for floats
+// >= 0 the u32 order is the float order, and an unsigned maximum needs no NaN
+// canonicalisation, so each step is one v_max_u32 with a DPP source
+QE_DEV float max16_abs(float v) {
+    unsigned u = __float_as_uint(v) & 0x7fffffffu;
+    u = max(u, dpp_u<QE_DPP_XOR1>(u));
+    u = max(u, dpp_u<QE_DPP_XOR2>(u));
+    u = max(u, dpp_u<QE_DPP_HMIRROR>(u));
+    return __uint_as_float(max(u, dpp_u<QE_DPP_MIRROR>(u)));
+}
 // maximum within aligned groups of 32 lanes
 QE_DEV float max32(float v) {
     unsigned a, b;

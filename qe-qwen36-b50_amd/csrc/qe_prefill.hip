@@ -404,7 +404,9 @@ __device__ __forceinline__ void expert_tile(const GemmTileArgs &a, const int4 it
         float *amax = utile + 2 * 16 * NT * 16;                  // [2][16 NT] |h| maxima per half
         uint8_t *htile = (uint8_t *)(amax + 2 * 16 * NT);         // [16 NT][32] int8 h, operand order
         float *stile = (float *)(htile + 16 * NT * 32);          // [16 NT] block scales
-        static_assert((2 * 16 * 16 + 2 * 16 + 32 + 1) * NT * 4 <= LY::ACT_SZ, "the epilogue fits the free stage");
+        float *itile = stile + 16 * NT;                          // [16 NT] their inverses
+        static_assert((2 * 16 * 16 * 4 + 2 * 16 * 4 + 16 * 32 + 2 * 16 * 4) * NT <= LY::ACT_SZ,
+                      "the epilogue fits the free stage");
         const int rs = wv & 1;
         if (wv >= 2) {
 #pragma unroll
@@ -421,9 +423,15 @@ __device__ __forceinline__ void expert_tile(const GemmTileArgs &a, const int4 it
                 for (int i = 0; i < 4; ++i) {
                     const int mi = 16 * t + 4 * g + i;
                     h[t][i] = silu_mul(acc[0][t][i], utile[(rs * 16 * NT + mi) * 16 + n]);
-                    m[t][i] = max16(fabsf(h[t][i]));
+                    m[t][i] = max16_abs(h[t][i]);
                     if (n == 0) amax[rs * 16 * NT + mi] = m[t][i];
                 }
+        }
+        __syncthreads();
+        if (tid < 16 * NT) { // the block's scale and its inverse, once per pair
+            float d;
+            itile[tid] = quant_scale_inv(fmaxf(amax[tid], amax[16 * NT + tid]), d);
+            stile[tid] = d;
         }
         __syncthreads();
         if (wv < 2) {
@@ -435,10 +443,7 @@ __device__ __forceinline__ void expert_tile(const GemmTileArgs &a, const int4 it
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const int mi = 16 * t + 4 * g + i;
-                    float d;
-                    const float id = quant_scale_inv(fmaxf(m[t][i], amax[(rs ^ 1) * 16 * NT + mi]), d);
-                    htile[mi * 32 + (n >> 2) * 8 + (n & 3) + 4 * rs] = (uint8_t)quant_one(h[t][i], id);
-                    if (n == 0 && rs == 0) stile[mi] = d;
+                    htile[mi * 32 + (n >> 2) * 8 + (n & 3) + 4 * rs] = (uint8_t)quant_one(h[t][i], itile[mi]);
                 }
         }
         __syncthreads();
@@ -470,7 +475,7 @@ __device__ __forceinline__ void expert_tile(const GemmTileArgs &a, const int4 it
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 h[t][i] = silu_mul(acc[0][t][i], acc[1][t][i]);
-                m[t][i] = max16(fabsf(h[t][i]));
+                m[t][i] = max16_abs(h[t][i]);
                 if (n == 0) amax[wv][16 * t + 4 * g + i] = m[t][i];
             }
         __syncthreads();
@@ -480,16 +485,23 @@ __device__ __forceinline__ void expert_tile(const GemmTileArgs &a, const int4 it
         // and stored 16 bytes per thread, instead of one byte per lane and value.
         uint8_t *htile = sm.raw + LY::ACT + (NCH & 1) * LY::ACT_SZ + 4 * QE_MFMA_MC * 4; // [16 NT][64]
         float *stile = (float *)(htile + 16 * NT * 64);                                  // [16 NT][2]
-        static_assert(4 * QE_MFMA_MC * 4 + 16 * NT * (64 + 8) <= LY::ACT_SZ, "h tile fits the free stage");
+        float *itile = stile + 16 * NT * 2;                                              // [2][16 NT] inverses
+        static_assert(4 * QE_MFMA_MC * 4 + 16 * NT * (64 + 8 + 8) <= LY::ACT_SZ, "h tile fits the free stage");
+        if (tid < 2 * 16 * NT) { // block (jb % 2 = wave pair) scale and its inverse, once per pair
+            const int pr = tid / (16 * NT), mi = tid % (16 * NT);
+            float d;
+            itile[tid] = quant_scale_inv(fmaxf(amax[2 * pr][mi], amax[2 * pr + 1][mi]), d);
+            stile[mi * 2 + pr] = d;
+        }
+        __syncthreads();
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
+            const float4 id4 = *(const float4 *)(itile + (wv >> 1) * 16 * NT + 16 * t + 4 * g);
+            const float id[4] = {id4.x, id4.y, id4.z, id4.w};
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int mi = 16 * t + 4 * g + i;
-                float d;
-                const float id = quant_scale_inv(fmaxf(m[t][i], amax[wv ^ 1][mi]), d);
-                htile[mi * 64 + (n >> 2) * 16 + (jb & 1) * 8 + (n & 3) + 4 * half] = (uint8_t)quant_one(h[t][i], id);
-                if (n == 0 && half == 0) stile[mi * 2 + (jb & 1)] = d;
+                htile[mi * 64 + (n >> 2) * 16 + (jb & 1) * 8 + (n & 3) + 4 * half] = (uint8_t)quant_one(h[t][i], id[i]);
             }
         }
         __syncthreads();
