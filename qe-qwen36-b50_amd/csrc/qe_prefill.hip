@@ -103,11 +103,11 @@ QE_DEV float4 ld_sc1_f4(const void *p) {
 // quads; loads are never predicated (the last refills wrap to the first blocks)
 // and each refill takes an offset that depends on the last read of its slot,
 // so it is issued 8 blocks ahead of its use into the slot's own registers.
-// The four waves of a workgroup share the item's pairs: each turn's activations
-// (256 bytes of K per pair) and block scales, and the weight scales of the
+// The four waves of a workgroup share the item's pairs: each quad's activations
+// (128 bytes of K per pair) and block scales, and the weight scales of the
 // workgroup's rows, are loaded once per workgroup into a double-buffered LDS
-// stage (issued a turn ahead, stored and published by one barrier at the end of
-// the turn), and every wave reads its A operands from there.
+// stage (issued a quad ahead, stored and published by one barrier at the end of
+// the quad), and every wave reads its A operands from there.
 typedef unsigned qe_u32x2 __attribute__((ext_vector_type(2)));
 typedef unsigned qe_u32x4 __attribute__((ext_vector_type(4)));
 
@@ -122,18 +122,24 @@ QE_DEV void transpose_rows4(uint32_t d[4]) {
 
 // LDS of one (NC, NT) tile, in bytes from the start of ExpertSmem::raw:
 //   weight scales of the workgroup's rows, whole K: fp16 [block][wave][n][group];
-//   two stages of the item's activations for one turn: [pair][256 bytes], the
-//     16-byte chunk q of pair m stored at chunk q ^ (m % 16) -- the sixteen rows a
-//     lane group reads in one instruction fall in sixteen different bank groups;
-//   two stages of their block scales for the turn: fp32 [block of the turn][pair].
+//   two stages of the item's activations for one quad (4 blocks): [pair][128 bytes],
+//     the 16-byte chunk q of pair m stored at chunk q ^ (m / 2 % 8) -- the sixteen
+//     rows a lane group reads in one instruction fall in sixteen different bank
+//     groups; a stage also holds the gate/up epilogue (EPI bytes) at the end;
+//   two stages of their block scales: fp32 [block of the quad][pair].
+// Stages of a quad rather than a turn keep a big item's workgroup at 34 KB, so
+// that four fit a CU.
+constexpr int qe_cmax(int a, int b) { return a > b ? a : b; }
 template <bool GU, int NC, int NT> struct TileLds {
     static constexpr int NB = (GU ? QE_D : QE_FF_EXP) / 32;
     static constexpr int DW = 0, DW_SZ = NB * 4 * 16 * NC * 2;
-    static constexpr int ACT = DW + DW_SZ, ACT_SZ = 16 * NT * 256;
-    static constexpr int XS = ACT + 2 * ACT_SZ, XS_SZ = 8 * 16 * NT * 4;
+    static constexpr int EPI = !GU ? 0
+                               : NC == 1 ? (2 * 16 * 16 * 4 + 2 * 16 * 4 + 16 * 32 + 2 * 16 * 4) * NT
+                                         : 4 * QE_MFMA_MC * 4 + 16 * NT * (64 + 8 + 8);
+    static constexpr int ACT = DW + DW_SZ, ACT_SZ = qe_cmax(16 * NT * 128, EPI);
+    static constexpr int XS = ACT + 2 * ACT_SZ, XS_SZ = 4 * 16 * NT * 4;
     static constexpr int SIZE = XS + 2 * XS_SZ;
 };
-constexpr int qe_cmax(int a, int b) { return a > b ? a : b; }
 template <bool GU> struct ExpertSmem {
     static constexpr int SIZE = qe_cmax(TileLds<GU, 2, 4>::SIZE, qe_cmax(TileLds<GU, 2, 2>::SIZE, TileLds<GU, 2, 1>::SIZE));
     static_assert(TileLds<GU, 1, 2>::SIZE <= SIZE, "the one-matrix gate/up waves fit as well");
@@ -214,38 +220,42 @@ __device__ __forceinline__ void expert_tile(const GemmTileArgs &a, const int4 it
     if (tid < QE_MFMA_MC) s_pair[tid] = tid < it.z ? a.pairs[it.y + tid] : -1;
     __syncthreads();
 
-    // Stage roles of this thread, per turn:
-    //   activations: pair m = 16 r + tid / 16, chunk q = tid % 16 of the turn, r < NT
+    // Stage roles of this thread, per quad:
+    //   activations: pair m = 32 r + tid / 8, chunk q = tid % 8 of the quad, m < 16 NT
     //     (padding pairs load pair 0's row; their scales are 0);
-    //   activation scales (tid >= 256 - 32 NT): blocks 4 h .. 4 h + 3 of the turn of pair m.
-    uint32_t act_off[NT];
+    //   activation scales (tid >= 256 - 16 NT): the quad's four blocks of pair m.
+    constexpr int NPASS = (16 * NT + 31) / 32;
+    uint32_t act_off[NPASS];
 #pragma unroll
-    for (int r = 0; r < NT; ++r) {
-        const int p = s_pair[16 * r + (tid >> 4)];
-        act_off[r] = (uint32_t)((p < 0 ? s_pair[0] : p) / a.a_row_div) * KD + 16 * (tid & 15);
+    for (int r = 0; r < NPASS; ++r) {
+        const int m = 32 * r + (tid >> 3), p = m < 16 * NT ? s_pair[m] : -1;
+        act_off[r] = (uint32_t)((p < 0 ? s_pair[0] : p) / a.a_row_div) * KD + 16 * (tid & 7);
     }
-    const int act_st = (tid >> 4) * 256 + (((tid & 15) ^ ((tid >> 4) & 15)) << 4); // + 16 r * 256
-    const int xs_i = tid - (256 - 32 * NT), xs_m = xs_i >> 1, xs_h = xs_i & 1;
-    const bool xs_role = xs_i >= 0;
+    const bool act_role = 32 * (NPASS - 1) + (tid >> 3) < 16 * NT; // the last pass (all passes when NT > 1)
+    const int act_st = (tid >> 3) * 128 + (((tid & 7) ^ ((tid >> 4) & 7)) << 4); // + 32 r * 128
+    const int xs_m = tid - (256 - 16 * NT);
+    const bool xs_role = xs_m >= 0;
     const int xs_p = xs_role ? s_pair[xs_m] : -1;
-    const float4 *xs_src = (const float4 *)(a.as + (size_t)((xs_p < 0 ? 0 : xs_p) / a.a_row_div) * NB + 4 * xs_h);
-    uint4 sa[NT];
+    const float4 *xs_src = (const float4 *)(a.as + (size_t)((xs_p < 0 ? 0 : xs_p) / a.a_row_div) * NB);
+    uint4 sa[NPASS];
     float4 sxs = make_float4(0.f, 0.f, 0.f, 0.f);
-    auto stage_load = [&](int ch) {
+    auto stage_load = [&](int qq) {
 #pragma unroll
-        for (int r = 0; r < NT; ++r) sa[r] = ld128(ar, act_off[r], 256 * ch);
-        if (xs_p >= 0) sxs = xs_src[2 * ch];
+        for (int r = 0; r < NPASS; ++r)
+            if (r + 1 < NPASS || act_role) sa[r] = ld128(ar, act_off[r], 128 * qq);
+        if (xs_p >= 0) sxs = xs_src[qq];
     };
     auto stage_store = [&](int s) {
         uint8_t *act = lds + LY::ACT + s * LY::ACT_SZ;
 #pragma unroll
-        for (int r = 0; r < NT; ++r) *(uint4 *)(act + 16 * r * 256 + act_st) = sa[r];
+        for (int r = 0; r < NPASS; ++r)
+            if (r + 1 < NPASS || act_role) *(uint4 *)(act + 32 * r * 128 + act_st) = sa[r];
         if (xs_role) {
             float *xs = (float *)(lds + LY::XS + s * LY::XS_SZ) + xs_m;
-            xs[(4 * xs_h + 0) * 16 * NT] = sxs.x;
-            xs[(4 * xs_h + 1) * 16 * NT] = sxs.y;
-            xs[(4 * xs_h + 2) * 16 * NT] = sxs.z;
-            xs[(4 * xs_h + 3) * 16 * NT] = sxs.w;
+            xs[0 * 16 * NT] = sxs.x;
+            xs[1 * 16 * NT] = sxs.y;
+            xs[2 * 16 * NT] = sxs.z;
+            xs[3 * 16 * NT] = sxs.w;
         }
     };
     stage_load(0);
@@ -271,12 +281,15 @@ __device__ __forceinline__ void expert_tile(const GemmTileArgs &a, const int4 it
 
     for (int ch = 0; ch < NCH; ++ch) {
         const int nx = ch + 1 < NCH ? ch + 1 : 0;
-        const uint8_t *act = lds + LY::ACT + (ch & 1) * LY::ACT_SZ;
-        const float *xsl = (const float *)(lds + LY::XS + (ch & 1) * LY::XS_SZ);
-        if (ch + 1 < NCH) stage_load(ch + 1); // next turn's stage, a turn ahead
-        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int qs = 0; qs < 2; ++qs) {
+            // quad qq = 2 ch + qs reads stage qs; the next quad's stage is loaded a quad ahead
+            const int qq = 2 * ch + qs;
+            const bool more = qq + 1 < 2 * NCH;
+            const uint8_t *act = lds + LY::ACT + qs * LY::ACT_SZ;
+            const float *xsl = (const float *)(lds + LY::XS + qs * LY::XS_SZ);
+            if (more) stage_load(qq + 1);
+            __builtin_amdgcn_sched_barrier(0);
             uint32_t cw[NC][4]; // [group][block of the quad]: the lane's code dword
 #pragma unroll
             for (int c = 0; c < NC; ++c) {
@@ -301,14 +314,14 @@ __device__ __forceinline__ void expert_tile(const GemmTileArgs &a, const int4 it
             }
 #pragma unroll
             for (int jp = 0; jp < 2; ++jp) {
-                // pair slot: blocks 4 qs + 2 jp, +1 of the turn; one 16-byte LDS read per tile
-                const int ps = 2 * qs + jp;
+                // blocks 2 jp, 2 jp + 1 of the quad: one 16-byte LDS read per tile
                 uint4 av2[NT];
 #pragma unroll
-                for (int t = 0; t < NT; ++t) av2[t] = *(const uint4 *)(act + (16 * t + n) * 256 + (((4 * ps + g) ^ n) << 4));
+                for (int t = 0; t < NT; ++t)
+                    av2[t] = *(const uint4 *)(act + (16 * t + n) * 128 + (((4 * jp + g) ^ (n >> 1)) << 4));
 #pragma unroll
                 for (int jj = 0; jj < 2; ++jj) {
-                    const int j = 2 * jp + jj, s = 4 * qs + j; // block s of the turn
+                    const int j = 2 * jp + jj, s = 4 * qs + j; // block j of the quad, s of the turn
                     long bv[NC];
 #pragma unroll
                     for (int c = 0; c < NC; ++c) {
@@ -348,7 +361,7 @@ __device__ __forceinline__ void expert_tile(const GemmTileArgs &a, const int4 it
                             const i32x4 mag = {QE_I2F_MAGIC_BITS, QE_I2F_MAGIC_BITS, QE_I2F_MAGIC_BITS, QE_I2F_MAGIC_BITS};
                             P[c] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bv[c], mag, 0, 0, 0);
                         }
-                        const float4 x4 = *(const float4 *)(xsl + s * 16 * NT + 16 * t + 4 * g);
+                        const float4 x4 = *(const float4 *)(xsl + j * 16 * NT + 16 * t + 4 * g);
 #pragma unroll
                         for (int c = 0; c < NC; ++c) {
                             acc[c][t][0] = fmaf(fmaf(__int_as_float(P[c][0]), dwf[c], cng[c]), x4.x, acc[c][t][0]);
@@ -366,13 +379,14 @@ __device__ __forceinline__ void expert_tile(const GemmTileArgs &a, const int4 it
                             asm volatile("" : "+v"(acc[c][t][0]), "+v"(acc[c][t][1]), "+v"(acc[c][t][2]), "+v"(acc[c][t][3]));
                 }
             }
-        }
-        if (ch + 1 < NCH) {
-            // the other stage was last read in turn ch - 1, before the previous barrier
-            stage_store((ch + 1) & 1);
-            __syncthreads();
+            if (more) {
+                // the other stage was last read in quad qq - 1, before the previous barrier
+                stage_store(qs ^ 1);
+                __syncthreads();
+            }
         }
     }
+    // the last quad (odd) read stage 1: the epilogue works in stage 0
 
     // lane holds rows 16 t + 4 g + i, column n of each group
     if constexpr (GU && NC == 4) {
@@ -398,8 +412,8 @@ __device__ __forceinline__ void expert_tile(const GemmTileArgs &a, const int4 it
         }
     } else if constexpr (GU && NC == 1) {
         // 32-block yb of h: rows 16 rs + n, rs = wv % 2, from gate wave rs and up wave
-        // 2 + rs.  All of it goes through the stage the last turn did not read.
-        uint8_t *fs = sm.raw + LY::ACT + (NCH & 1) * LY::ACT_SZ;
+        // 2 + rs.  All of it goes through stage 0, which the last quad did not read.
+        uint8_t *fs = sm.raw + LY::ACT;
         float *utile = (float *)fs;                              // [2][16 NT pairs][16] the up dots
         float *amax = utile + 2 * 16 * NT * 16;                  // [2][16 NT] |h| maxima per half
         uint8_t *htile = (uint8_t *)(amax + 2 * 16 * NT);         // [16 NT][32] int8 h, operand order
@@ -466,8 +480,8 @@ __device__ __forceinline__ void expert_tile(const GemmTileArgs &a, const int4 it
         // h rows 16 (4 yb + wv) + n: half (wv & 1) of 32-block jb
         const int jb = yb * 2 + (wv >> 1), half = wv & 1;
         // each wave's |h| maximum per pair, in the activation stage the last turn
-        // did not read (its last reader passed the barrier that ended turn NCH - 2)
-        float(*amax)[QE_MFMA_MC] = (float(*)[QE_MFMA_MC])(sm.raw + LY::ACT + (NCH & 1) * LY::ACT_SZ);
+        // did not read (stage 0: its last reader passed the barrier that ended quad 2 NCH - 2)
+        float(*amax)[QE_MFMA_MC] = (float(*)[QE_MFMA_MC])(sm.raw + LY::ACT);
         static_assert(4 * QE_MFMA_MC * 4 <= LY::ACT_SZ, "maxima fit one stage");
         float h[NT][4], m[NT][4];
 #pragma unroll
@@ -483,7 +497,7 @@ __device__ __forceinline__ void expert_tile(const GemmTileArgs &a, const int4 it
         // row in the operand layout (blocks 2 yb, 2 yb + 1), and its two block scales are
         // adjacent: both are assembled in LDS (after the maxima, in the same free stage)
         // and stored 16 bytes per thread, instead of one byte per lane and value.
-        uint8_t *htile = sm.raw + LY::ACT + (NCH & 1) * LY::ACT_SZ + 4 * QE_MFMA_MC * 4; // [16 NT][64]
+        uint8_t *htile = sm.raw + LY::ACT + 4 * QE_MFMA_MC * 4; // [16 NT][64]
         float *stile = (float *)(htile + 16 * NT * 64);                                  // [16 NT][2]
         float *itile = stile + 16 * NT * 2;                                              // [2][16 NT] inverses
         static_assert(4 * QE_MFMA_MC * 4 + 16 * NT * (64 + 8 + 8) <= LY::ACT_SZ, "h tile fits the free stage");
@@ -578,7 +592,7 @@ template <bool GU> QE_DEV void expert_unit(const GemmTileArgs &a, int b, ExpertS
 template <bool GU> constexpr int expert_max_wg(int np) {
     return expert_rg<GU>() * (((np / (QE_MFMA_MC / 2 + 1) + 1 + QE_N_EXPERT) + 7) & ~7);
 }
-__global__ __launch_bounds__(256, 2) void k_expert_gu(GemmTileArgs a) {
+__global__ __launch_bounds__(256, 4) void k_expert_gu(GemmTileArgs a) {
     __shared__ ExpertSmem<true> sm;
     expert_unit<true>(a, blockIdx.x, sm);
 }
@@ -1294,7 +1308,7 @@ __global__ __launch_bounds__(256, 2) void k_expert_dn(GemmTileArgs a, int nr, co
 #ifndef QE_FUSE_T
 #define QE_FUSE_T 4096
 #endif
-__global__ __launch_bounds__(256, 2) void k_expert_gudn(GemmTileArgs gu, GemmTileArgs dn, int nshx,
+__global__ __launch_bounds__(256, 4) void k_expert_gudn(GemmTileArgs gu, GemmTileArgs dn, int nshx,
                                                         const _Float16 *hhl, int T, const uint8_t *Wsd, float *sd) {
     __shared__ union {
         ExpertSmem<true> g;
