@@ -501,6 +501,7 @@ int qe_moe_dispatch_noalloc(const int32_t *ids, int T, int32_t *off, int32_t *pa
     return QE_OK;
 }
 static_assert(QE_MOE_DISPATCH_NOALLOC_T_MAX == QE_DISPATCH_NOALLOC_T_MAX, "header and library limits agree");
+static_assert(QE_MOE_T_MAX == QE_LAYER_T_MAX, "header and library limits agree");
 
 int qe_moe_get_logits(qe_moe_ctx *c, int T, float *logits, void *stream) {
     if (!c || !logits || T <= 0 || T > c->t_max) return fail(QE_ERR_ARG, "get_logits: bad argument");

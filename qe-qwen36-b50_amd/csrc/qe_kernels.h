@@ -105,6 +105,9 @@ hipError_t qe_launch_decode(const QeDecodeArgs &a, hipStream_t st);
 
 // Launchers (qe_kernels.hip).  xin: layer input; post_norm: nullptr = input is
 // already normalised; x2: residual added to the output or nullptr.
+// tokens of the largest call (the API's limit): the down epilogue's 32-bit store
+// offsets rely on its pair count staying below 2^19
+#define QE_LAYER_T_MAX 65536
 hipError_t qe_launch_layer(const QeLayerPtrs &L, const QeScratch &S, const float *xin, bool norm, const float *x2,
                            float *out, int T, hipStream_t st, const float *exit_norm = nullptr,
                            float *exit_xn = nullptr);

@@ -1207,8 +1207,14 @@ __device__ __forceinline__ void dn_tile(const GemmTileArgs &a, const int4 it, co
             // n ^ 1 swap a value, so the even one stores rows n, n + 1 and the odd one rows
             // 15 + n, 16 + n as 8-byte pairs: the 16 lanes of a pair write its 128 bytes
             // as one line instead of two half lines
+            // The store address is a wave-uniform base (row group, wave) plus a 32-bit
+            // lane offset pm * 8192 + 4 col (pm < 2^19 pairs), one VALU instruction per
+            // store where 64-bit address arithmetic took six.
             const int rg = rg0 + (qi >> 2);
             const bool odd = n & 1;
+            static_assert(QE_D * 4 == 1 << 13 && QE_LAYER_T_MAX * QE_K_USED <= 1 << 19, "offsets fit 32 bits");
+            const char *ybase = (const char *)(a.yp + 128 * rg + 32 * __builtin_amdgcn_readfirstlane(wv));
+            const uint32_t col4 = 4u * (odd ? 15 + n : n);
 #pragma unroll
             for (int t = 0; t < NT; ++t)
 #pragma unroll
@@ -1217,10 +1223,9 @@ __device__ __forceinline__ void dn_tile(const GemmTileArgs &a, const int4 it, co
                     const float w = sm.w[m];
                     const float y0 = w * acc[0][t][i], y1 = w * acc[1][t][i];
                     const float p0 = dpp_f<QE_DPP_XOR1>(y0), p1 = dpp_f<QE_DPP_XOR1>(y1);
-                    if (pm >= 0) {
-                        float *yrow = a.yp + (size_t)pm * QE_D + 128 * rg + 32 * wv;
-                        *(float2 *)(yrow + (odd ? 15 + n : n)) = odd ? make_float2(p1, y1) : make_float2(y0, p0);
-                    }
+                    if (pm >= 0)
+                        *(float2 *)(ybase + (((uint32_t)pm << 13) | col4)) =
+                            odd ? make_float2(p1, y1) : make_float2(y0, p0);
 #pragma unroll
                     for (int c = 0; c < NC; ++c) acc[c][t][i] = 0.f;
                 }
