@@ -178,7 +178,7 @@ __global__ __launch_bounds__(1024) void k_disp_hist(const int32_t *ids, int np, 
 __global__ __launch_bounds__(1024) void k_disp_scatter(const int32_t *ids, int np, const int32_t *chunk_hist, int nch,
                                                        int tc, int32_t *off_out, int32_t *pairs, int4 *items,
                                                        int32_t *n_items, int32_t *item_done) {
-    __shared__ int s_before[QE_N_EXPERT], s_off[QE_N_EXPERT], s_cnt[QE_N_EXPERT], s_scan[QE_N_EXPERT];
+    __shared__ int s_before[QE_N_EXPERT], s_off[QE_N_EXPERT];
     __shared__ int s_w[16][QE_N_EXPERT];
     __shared__ int s_part[2][4][QE_N_EXPERT];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -199,64 +199,70 @@ __global__ __launch_bounds__(1024) void k_disp_scatter(const int32_t *ids, int n
     }
     for (int i = tid; i < 16 * QE_N_EXPERT; i += 1024) (&s_w[0][0])[i] = 0;
     __syncthreads();
+    // Exclusive prefix sums over the 256 experts (threads 0..255, four waves) of the
+    // pair counts and, for the work items of <= tc pairs, of each expert's big and
+    // small item counts: inclusive sums within each wave by shuffles, then the
+    // earlier waves' totals through LDS -- two barriers where Hillis-Steele scans over
+    // LDS took sixteen each.  Items: first every item of more than tc / 2 pairs (whole
+    // items and large remainders), then the small remainders, each class in expert
+    // order -- the longer items start first.
+    __shared__ int s_wt[4][3];
+    int cnt = 0, full = 0, rem = 0, nb = 0, ns = 0, ic = 0, ib = 0, is = 0;
     if (tid < QE_N_EXPERT) {
-        s_cnt[tid] = (s_part[0][0][tid] + s_part[0][1][tid]) + (s_part[0][2][tid] + s_part[0][3][tid]);
+        cnt = (s_part[0][0][tid] + s_part[0][1][tid]) + (s_part[0][2][tid] + s_part[0][3][tid]);
         s_before[tid] = (s_part[1][0][tid] + s_part[1][1][tid]) + (s_part[1][2][tid] + s_part[1][3][tid]);
+        full = cnt / tc;
+        rem = cnt % tc;
+        nb = full + (rem > tc / 2);
+        ns = rem > 0 && rem <= tc / 2;
+        ic = cnt;
+        ib = nb;
+        is = ns;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const int c2 = __shfl_up(ic, d), b2 = __shfl_up(ib, d), s2 = __shfl_up(is, d);
+            if (lane >= d) {
+                ic += c2;
+                ib += b2;
+                is += s2;
+            }
+        }
+        if (lane == 63) {
+            s_wt[wv][0] = ic;
+            s_wt[wv][1] = ib;
+            s_wt[wv][2] = is;
+        }
     }
     __syncthreads();
-    if (tid < 256) {
-        // exclusive scan of s_cnt over 256 experts (threads 0..255)
-        s_scan[tid] = s_cnt[tid];
+    int all_c = 0, all_b = 0, all_s = 0; // totals over the experts
+    if (tid < QE_N_EXPERT) {
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            if (w < wv) {
+                ic += s_wt[w][0];
+                ib += s_wt[w][1];
+                is += s_wt[w][2];
+            }
+            all_c += s_wt[w][0];
+            all_b += s_wt[w][1];
+            all_s += s_wt[w][2];
+        }
+        s_off[tid] = ic - cnt;
     }
     __syncthreads();
-    for (int o = 1; o < 256; o <<= 1) {
-        int v = 0;
-        if (tid < 256 && tid >= o) v = s_scan[tid - o];
-        __syncthreads();
-        if (tid < 256) s_scan[tid] += v;
-        __syncthreads();
-    }
-    if (tid < 256) s_off[tid] = s_scan[tid] - s_cnt[tid];
-    __syncthreads();
-    if (blockIdx.x == 0) {
-        if (tid < 256) off_out[tid] = s_off[tid];
-        if (tid == 0) off_out[QE_N_EXPERT] = s_scan[255];
-        // work items of <= tc pairs per expert: first every item of more than
-        // tc / 2 pairs (whole items and large remainders), then the small
-        // remainders, each class in expert order -- the longer items start first
-        __shared__ int s_nb[QE_N_EXPERT], s_ns[QE_N_EXPERT];
-        const int cnt = tid < 256 ? s_cnt[tid] : 0, full = cnt / tc, rem = cnt % tc;
-        const int nb = full + (rem > tc / 2), ns = rem > 0 && rem <= tc / 2;
-        if (tid < 256) {
-            s_nb[tid] = nb;
-            s_ns[tid] = ns;
+    if (blockIdx.x == 0 && tid < QE_N_EXPERT) {
+        const int off = ic - cnt, bb = ib - nb;
+        off_out[tid] = off;
+        if (tid == 0) off_out[QE_N_EXPERT] = all_c;
+        for (int c = 0; c < full; ++c) items[bb + c] = make_int4(tid, off + c * tc, tc, 0);
+        if (rem > tc / 2) items[bb + full] = make_int4(tid, off + full * tc, rem, 0);
+        if (ns) items[all_b + is - 1] = make_int4(tid, off + full * tc, rem, 0);
+        if (tid == QE_N_EXPERT - 1) {
+            n_items[0] = all_b + all_s;
+            n_items[1] = all_b;
         }
-        __syncthreads();
-        for (int o = 1; o < 256; o <<= 1) {
-            int vb = 0, vs = 0;
-            if (tid < 256 && tid >= o) {
-                vb = s_nb[tid - o];
-                vs = s_ns[tid - o];
-            }
-            __syncthreads();
-            if (tid < 256) {
-                s_nb[tid] += vb;
-                s_ns[tid] += vs;
-            }
-            __syncthreads();
-        }
-        if (tid < 256) {
-            const int bb = s_nb[tid] - nb, total_b = s_nb[255];
-            for (int c = 0; c < full; ++c) items[bb + c] = make_int4(tid, s_off[tid] + c * tc, tc, 0);
-            if (rem > tc / 2) items[bb + full] = make_int4(tid, s_off[tid] + full * tc, rem, 0);
-            if (ns) items[total_b + s_ns[tid] - 1] = make_int4(tid, s_off[tid] + full * tc, rem, 0);
-            if (tid == 255) {
-                n_items[0] = total_b + s_ns[255];
-                n_items[1] = total_b;
-            }
-            if (item_done) // the fused gate/up + down launch counts its gate/up workgroups per item
-                for (int i = tid; i < total_b + s_ns[255]; i += 256) item_done[i] = 0;
-        }
+        if (item_done) // the fused gate/up + down launch counts its gate/up workgroups per item
+            for (int i = tid; i < all_b + all_s; i += QE_N_EXPERT) item_done[i] = 0;
     }
     const int p = blockIdx.x * 1024 + tid;
     const bool valid = p < np;
@@ -274,7 +280,8 @@ __global__ __launch_bounds__(1024) void k_disp_scatter(const int32_t *ids, int n
     if (valid) {
         int cross = 0;
         for (int w = 0; w < wv; ++w) cross += s_w[w][e];
-        pairs[s_off[e] + s_before[e] + cross + rank] = p;
+        const int dst = s_off[e] + s_before[e] + cross + rank; // < np by construction; kept in bounds regardless
+        if (dst < np) pairs[dst] = p;
     }
 }
 
