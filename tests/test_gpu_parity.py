@@ -168,18 +168,13 @@ def test_cfg3_prefill_512(ctx, torch_cuda):
 
 
 def test_cfg4_prefill_8192_skewed(ctx, torch_cuda):
-    say("config 4: prefill 8192, Zipf s=1.3 (routing on all tokens, outputs on a sample)")
+    # every token: logits and ids bit for bit, the dispatch, and the outputs (the
+    # oracle's full layer at 8192 tokens takes seconds on the host's cores)
+    say("config 4: prefill 8192, Zipf s=1.3 (routing, dispatch and outputs on all tokens)")
     x = O.gen_x(SEED, 4, 8192)
     L, g = run_gpu(torch_cuda, ctx, 1, 1.3, x)
-    lg = O.router(x, L.router, L.bias)
-    assert np.array_equal(g["logits"].view(np.uint32), lg.view(np.uint32))
-    ids, _, _ = O.topk(lg)
-    assert np.array_equal(g["ids"], ids)
-    off, pairs = O.dispatch(ids)
-    assert np.array_equal(g["off"], off) and np.array_equal(g["pairs"], pairs)
-    sample = np.sort(np.random.default_rng(4).choice(8192, 96, replace=False))
-    check_layer(L, g, x, sample=sample)
-    cnt = np.diff(off)
+    o = check_layer(L, g, x)
+    cnt = np.diff(o["off"])
     say(f"  distinct {np.count_nonzero(cnt)}, max/expert {cnt.max()}, <4 tokens {int(((cnt > 0) & (cnt < 4)).sum())}")
 
 
