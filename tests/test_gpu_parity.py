@@ -181,8 +181,8 @@ def test_cfg4_prefill_8192_skewed(ctx, torch_cuda):
 def test_prefill_at_abi_max_T(torch_cuda):
     """T = QE_MOE_T_MAX (65,536 tokens, 524,288 pairs), the largest call the ABI
     accepts, with config 4's Zipf s=1.3 bias: logits, ids, offsets and the
-    permutation on every token, outputs on a sample (the oracle's full layer at
-    this T would take many minutes on the host)."""
+    permutation on every token, outputs on a sample of 4096 tokens spread over
+    the call (each token's output depends on its own row only)."""
     torch = torch_cuda
     T = qe_moe.QE_MOE_T_MAX
     m = qe_moe.MoE(n_layers=1, t_max=T)
@@ -204,7 +204,7 @@ def test_prefill_at_abi_max_T(torch_cuda):
         assert np.array_equal(g["ids"], ids), "routing ids differ"
         off, pairs = O.dispatch(ids)
         assert np.array_equal(g["off"], off) and np.array_equal(g["pairs"], pairs), "dispatch differs"
-        sample = np.sort(np.random.default_rng(65).choice(T, 64, replace=False))
+        sample = np.sort(np.random.default_rng(65).choice(T, 4096, replace=False))
         check_layer(L, g, x, sample=sample)
         cnt = np.diff(off)
         say(f"  distinct {np.count_nonzero(cnt)}, max/expert {cnt.max()}, <4 tokens {int(((cnt > 0) & (cnt < 4)).sum())}")
